@@ -1,0 +1,295 @@
+"""Benchmark of the W4A16 hot path on one MI355X ([3]).
+
+    python bench.py [--gpus 1] [--steps 160] [--warmup 32]
+
+A *step* is one M=1 (decode) pass over the seven linears of one
+Llama-3.2-1B decoder block (q/o 2048x2048, k/v 512x2048, gate/up 8192x2048,
+down 2048x8192; N x K), G=128, bf16 activations, as ONE grouped launch
+(``w4a16_matmul_grouped``).  Steps rotate over 16 distinct seeded weight sets
+(16 x 32.3 MB > the 256 MB Infinity Cache) so weights stream from HBM.
+Inputs are resident in HBM before the timed region; launches are replayed
+from a HIP graph.
+
+Printed (last line, JSON): ``value`` = algorithmic HBM bytes of the block
+(sum N*K/2 + 4*N*K/G + 2*K + 2*N = 32,397,312 B) / time per step, in GB/s,
+plus ``roofline`` for the dominant kernel (the grouped decode GEMV, per-launch
+duration from HIP events recorded around each launch inside the graph) and
+``cpu_baseline`` (the CPU oracle, a numpy port of the reference's torch CPU
+dequantize-then-matmul path, timed on a bounded sample).  Extra fields carry
+the per-linear (7-launch) decode block, the split-K M=16 block, the M=2048
+prefill TFLOPS with a hipBLASLt bf16 reference, and the quantize kernel.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "itmo-final-project_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+LINEARS = [("q_proj", 2048, 2048), ("k_proj", 512, 2048), ("v_proj", 512, 2048), ("o_proj", 2048, 2048),
+           ("gate_proj", 8192, 2048), ("up_proj", 8192, 2048), ("down_proj", 2048, 8192)]
+G = 128
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
+METRIC = "µs & HBM GB/s per 7-linear block at M=1; W4A16 TFLOPS at M=2048"
+
+
+def block_bytes(M: int, g: int = G) -> int:
+    return sum(N * K // 2 + 4 * N * K // g + 2 * M * K + 2 * M * N for _, N, K in LINEARS)
+
+
+def block_flops(M: int) -> int:
+    return sum(2 * M * N * K for _, N, K in LINEARS)
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def graph_of(fn, stream):
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        fn()  # warm-up outside the graph
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, reps: int, stream) -> float:
+    """ms per replay, events recorded on the replay stream, bracketed by syncs."""
+    import torch
+
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def per_launch_ms(launches, stream) -> float | None:
+    """Mean GPU duration of each launch, from event pairs captured around every
+    launch inside one graph (no host gaps between the pair)."""
+    import torch
+
+    def ev():
+        try:  # external=True: a real timestamp node inside the captured graph
+            return torch.cuda.Event(enable_timing=True, external=True)
+        except TypeError:
+            return torch.cuda.Event(enable_timing=True)
+
+    evs = [(ev(), ev()) for _ in launches]
+
+    def body():
+        for (a, b), fn in zip(evs, launches):
+            a.record(stream)
+            fn()
+            b.record(stream)
+
+    try:
+        g = graph_of(body, stream)
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
+        ts = [a.elapsed_time(b) for a, b in evs]
+    except Exception as e:  # event nodes not supported in graphs on this stack
+        log(f"per-launch events inside a graph unavailable ({e!r}); using the replay average")
+        return None
+    if min(ts) <= 0:
+        log(f"per-launch events inside a graph gave non-positive durations {ts[:4]}; using the replay average")
+        return None
+    return sum(ts) / len(ts)
+
+
+def cpu_baseline(packed, xs_bits, sample_passes: int) -> dict:
+    """The CPU oracle (numpy port of the reference's torch CPU path:
+    dequantize_int4_ref(..., bf16) then x @ W_hat^T) over the M=1 block.
+    ``packed``: per linear (qweight int32, scales/zeros fp16 bits) as numpy."""
+    import numpy as np
+
+    from oracle import w4a16_oracle as O
+
+    ts = []
+    for _ in range(sample_passes):
+        t0 = time.perf_counter()
+        for (qw, s, z), xb in zip(packed, xs_bits):
+            O.w4a16_matmul(xb, "bf16", qw, s, z, accumulate="f32")
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    return {"value": round(block_bytes(1) / t / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle, dequantize(bf16)+matmul over the 7-linear block at M=1, G=128, "
+                      f"median of {sample_passes} passes ({t * 1e3:.1f} ms per block)",
+            "ms_per_block": round(t * 1e3, 3)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=160)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--sets", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-passes", type=int, default=5)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the W4A16 path has no collective); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import int4_hip
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    stream = torch.cuda.Stream(dev)
+    nsets = args.sets
+    gen = torch.Generator(device=dev).manual_seed(1234)
+
+    # ---------------------------------------------------------------- inputs
+    log(f"generating {nsets} weight sets ...")
+    w16 = [[(torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _, N, K in LINEARS]
+           for _ in range(nsets)]
+    packed = [[int4_hip.quantize_int4(w, G) for w in ws] for ws in w16]
+    xs1 = [[torch.randn((1, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
+           for _ in range(nsets)]
+    ys1 = [[torch.empty((1, N), device=dev, dtype=torch.bfloat16) for _, N, K in LINEARS] for _ in range(nsets)]
+    torch.cuda.synchronize()
+
+    # ------------------------------------------------- quantize kernel (load time)
+    def quant_set(i):
+        return lambda: [int4_hip.quantize_int4(w, G) for w in w16[i]]
+
+    gq = graph_of(lambda: [quant_set(i)() for i in range(nsets)], stream)
+    q_ms = time_graph(gq, 3, stream) / nsets
+    q_bytes = sum(2 * N * K + N * K // 2 + 4 * N * K // G for _, N, K in LINEARS)
+    del gq
+    del w16
+    torch.cuda.empty_cache()
+
+    # ------------------------------------------------- M=1 decode block: grouped launch
+    def grouped(i):
+        return lambda: int4_hip.w4a16_matmul_grouped(xs1[i], packed[i], out=ys1[i])
+
+    steps = max(nsets, (args.steps + nsets - 1) // nsets * nsets)
+    warm = max(1, args.warmup // nsets)
+    g_main = graph_of(lambda: [grouped(i)() for i in range(nsets)], stream)
+    time_graph(g_main, warm, stream)
+    ms_rot = time_graph(g_main, steps // nsets, stream)
+    ms_per_step = ms_rot / nsets
+    bytes1 = block_bytes(1)
+    value = bytes1 / (ms_per_step * 1e-3) / 1e9
+    kern_ms = per_launch_ms([grouped(i) for i in range(nsets)], stream)
+    kern_ms_src = "hip-events-around-each-launch-in-graph"
+    if kern_ms is None:
+        kern_ms, kern_ms_src = ms_per_step, "graph-replay-average"
+    achieved = bytes1 / (kern_ms * 1e-3) / 1e9
+
+    # ------------------------------------------------- M=1 per-linear launches (reference-comparable)
+    def single(i, j):
+        return lambda: int4_hip.w4a16_matmul(xs1[i][j], *packed[i][j])
+
+    per_lin = {}
+    for j, (name, N, K) in enumerate(LINEARS):
+        gj = graph_of(lambda j=j: [single(i, j)() for i in range(nsets)], stream)
+        time_graph(gj, 2, stream)
+        per_lin[name] = time_graph(gj, 10, stream) / nsets * 1e3
+        del gj
+    g7 = graph_of(lambda: [single(i, j)() for i in range(nsets) for j in range(len(LINEARS))], stream)
+    time_graph(g7, 2, stream)
+    ms7 = time_graph(g7, 10, stream) / nsets
+    del g7
+
+    # ------------------------------------------------- split-K M=16 block
+    xs16 = [torch.randn((16, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
+    g16 = graph_of(lambda: [int4_hip.w4a16_matmul(xs16[j], *packed[i][j]) for i in range(nsets)
+                            for j in range(len(LINEARS))], stream)
+    time_graph(g16, 2, stream)
+    ms16 = time_graph(g16, 5, stream) / nsets
+    del g16
+
+    # ------------------------------------------------- prefill M=2048
+    pre = {}
+    for M in (128, 512, 2048):
+        xsM = [torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
+        gp = graph_of(lambda: [int4_hip.w4a16_matmul(xsM[j], *packed[0][j]) for j in range(len(LINEARS))], stream)
+        time_graph(gp, 3, stream)
+        msM = time_graph(gp, 10, stream)
+        pre[M] = {"us_per_block": round(msM * 1e3, 2), "tflops": round(block_flops(M) / (msM * 1e-3) / 1e12, 2)}
+        del gp
+        if M == 2048:
+            w_deq = [int4_hip.dequantize_int4(*packed[0][j], torch.bfloat16) for j in range(len(LINEARS))]
+            gb = graph_of(lambda: [torch.nn.functional.linear(xsM[j], w_deq[j]) for j in range(len(LINEARS))], stream)
+            time_graph(gb, 3, stream)
+            msb = time_graph(gb, 10, stream)
+            pre[M]["hipblaslt_bf16_dequantized_us"] = round(msb * 1e3, 2)
+            pre[M]["hipblaslt_bf16_tflops"] = round(block_flops(M) / (msb * 1e-3) / 1e12, 2)
+            del gb, w_deq
+        del xsM
+    torch.cuda.synchronize()
+
+    # ------------------------------------------------- CPU baseline (rank 0, N=1)
+    cpu = None
+    if not args.no_cpu:
+        def bits(t):
+            return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+        packed0 = [(qw.cpu().numpy(), bits(s.cpu()), bits(z.cpu())) for qw, s, z in packed[0]]
+        cpu = cpu_baseline(packed0, [bits(x.cpu()) for x in xs1[0]], args.cpu_passes)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warm * nsets,
+        "ms_per_step": round(ms_per_step, 6),
+        "us_per_block": round(ms_per_step * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "Llama-3.2-1B decoder block: 7 W4A16 linears (q/k/v/o/gate/up/down), M=1 "
+                               "decode GEMV as one grouped launch, G=128, bf16 activations, "
+                               f"{nsets} rotated weight sets ({nsets * bytes1 / 1e6:.0f} MB)",
+                   "M": 1, "group_size": G, "weight_sets": nsets, "bytes_per_step": bytes1},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "w4::grouped_kernel<bf16>", "kernel_us": round(kern_ms * 1e3, 3),
+                     "kernel_time_source": kern_ms_src},
+        "cpu_baseline": cpu,
+        "decode_m1_per_linear_us": {k: round(v, 3) for k, v in per_lin.items()},
+        "decode_m1_7_launches_us_per_block": round(ms7 * 1e3, 3),
+        "decode_m1_7_launches_gbps": round(bytes1 / (ms7 * 1e-3) / 1e9, 1),
+        "splitk_m16_us_per_block": round(ms16 * 1e3, 3),
+        "splitk_m16_gbps": round(block_bytes(16) / (ms16 * 1e-3) / 1e9, 1),
+        "prefill": {str(k): v for k, v in pre.items()},
+        "prefill_m2048_tflops": pre[2048]["tflops"],
+        "prefill_m2048_mfma_frac": round(pre[2048]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
+        "quantize_us_per_block": round(q_ms * 1e3, 2),
+        "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
+        "device": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

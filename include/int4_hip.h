@@ -1,0 +1,139 @@
+/*
+ * int4_hip: C-ABI of the MI355X (gfx950) W4A16 quantize + GEMM library.
+ *
+ * The reference (homomorfism/itmo-final-project, package int4_triton) exposes
+ * this path as Python functions that launch Triton kernels; there is no FFI
+ * there.  Each entry point below replaces one of those launch sites, named in
+ * its comment (file:line in the reference).  A Python host package
+ * (itmo-final-project_amd/int4_hip) binds these symbols with ctypes and keeps
+ * the reference's Python names, argument meaning and assertions.
+ *
+ * Conventions (all entry points):
+ *  - Plain pointers, sizes and strides; strides are in ELEMENTS.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the default stream).
+ *    Work is enqueued on it; nothing synchronises with the host.
+ *  - The library never allocates or frees device memory.  Scratch memory
+ *    (split-K partial sums) is passed in as `workspace`.
+ *  - Half-precision tensors are passed as 16-bit patterns (uint16_t).
+ *  - Return 0 on success, a nonzero W4_ERR_* code on failure; the message of
+ *    the last failure on the calling thread is returned by w4_last_error().
+ *
+ * Storage layout (int4_triton/quantize.py:8-12):
+ *   qweight int32 [K/8, N] row-major, nibble i of word (k8, n) = row 8*k8+i of
+ *   W^T, i.e. bits 4i..4i+3;  scales, zeros fp16 [K/G, N] row-major.
+ */
+#ifndef INT4_HIP_H
+#define INT4_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W4_ABI_VERSION 1
+
+/* dtype codes */
+#define W4_DTYPE_BF16 0
+#define W4_DTYPE_FP16 1
+#define W4_DTYPE_FP32 2
+
+/* status codes */
+#define W4_OK 0
+#define W4_ERR_INVALID 1     /* bad shape, stride, dtype or group size       */
+#define W4_ERR_UNSUPPORTED 2 /* valid for the reference, not implemented    */
+#define W4_ERR_WORKSPACE 3   /* workspace missing or smaller than required   */
+#define W4_ERR_LAUNCH 4      /* HIP launch error (hipGetLastError)           */
+
+/* Library version; lets bindings reject a stale build. */
+int w4_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* w4_last_error(void);
+
+/*
+ * Group-wise asymmetric RTN int4 quantization of W[N, K] (bf16 or fp16, any
+ * strides) into freshly laid-out qweight int32 [K/8, N], scales/zeros fp16
+ * [K/G, N] (dense, row-major).  group_size: power of two, multiple of 8,
+ * dividing K; -1 means K (per-channel).  Bit-exact with the reference's torch
+ * implementation for every finite input.
+ * Replaces: int4_triton/quantize.py:67-96 (quantize_int4 and the launch of
+ * _quantize_int4_kernel, :21-64); semantics of quantize_int4_ref, :102-117.
+ */
+int w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K,
+                int64_t stride_wn, int64_t stride_wk, int group_size,
+                int32_t* qweight, uint16_t* scales, uint16_t* zeros, void* stream);
+
+/*
+ * W_hat[N, K] (dense, row-major) = round_once_to_out_dtype((q - z) * s),
+ * computed exactly in fp32.  out_dtype: W4_DTYPE_BF16/FP16/FP32.
+ * Replaces: int4_triton/quantize.py:128-135 (dequantize_int4_ref) as used by
+ * Int4Linear.dequantize (int4_triton/qlinear.py:39-40) and fake mode (:63-64).
+ */
+int w4_dequantize(const int32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
+                  int64_t N, int64_t K, int group_size, int out_dtype, void* out,
+                  void* stream);
+
+/*
+ * Bytes of workspace w4a16_gemm needs for this problem (0 when the chosen
+ * launch writes y directly).  Depends only on (M, N, K, group_size) and the
+ * device's compute-unit count, never on timing, so the split-K decomposition
+ * (and therefore every output bit) is the same in every process.
+ * Replaces: the per-call `partials` allocation, int4_triton/gemm.py:268.
+ */
+size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
+
+/*
+ * y[M, N] = x[M, K] @ W_hat^T with W_hat the dequantized int4 weight, fp32
+ * accumulation, y in x's dtype.  x: bf16/fp16, any strides (stride_xm,
+ * stride_xk).  qweight/scales/zeros dense row-major as above.  y: row stride
+ * ldy (>= N), unit column stride.  Launch regimes (same boundaries as the
+ * reference): M == 1 decode GEMV; 2 <= M <= 64 split-K with fp32 partials in
+ * `workspace` and a fixed-order reduce (bit-identical run to run); M > 64
+ * tiled MFMA GEMM.
+ * Replaces: int4_triton/gemm.py:303-309 (w4a16_matmul) and its dispatcher
+ * _matmul, :234-300 (kernels :74-157, :171-182, :185-220).
+ */
+int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+               int64_t stride_xm, int64_t stride_xk,
+               const int32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
+               int group_size, void* y, int64_t ldy,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * One problem of a grouped decode launch: y_i[M, N_i] = x_i[M, K_i] @ W_hat_i^T.
+ * x_i dense row-major [M, K_i]; y_i dense row-major [M, N_i].
+ */
+typedef struct w4a16_problem {
+  const void* x;
+  const int32_t* qweight;
+  const uint16_t* scales;
+  const uint16_t* zeros;
+  void* y;
+  int64_t N;
+  int64_t K;
+  int32_t group_size;
+  int32_t reserved;
+} w4a16_problem;
+
+#define W4_MAX_GROUPED 8
+
+/*
+ * Up to W4_MAX_GROUPED independent small-M (1 <= M <= 16) products in ONE
+ * kernel launch, all with the same activation dtype and M.  Each output
+ * column's reduction over K stays inside one workgroup (no workspace, no
+ * atomics), so results are bit-identical to w4a16_gemm's direct path only up
+ * to summation order, and bit-identical run to run.
+ * No single counterpart in the reference: it fuses the per-linear launches of
+ * int4_triton/gemm.py:245-264 that a decoder block issues back to back
+ * (q/k/v/o/gate/up/down, benchmarks/bench_gemm.py:18-26).
+ */
+int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
+                       void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INT4_HIP_H */

@@ -1,0 +1,385 @@
+// Group-wise asymmetric RTN int4 quantize/pack and the exact dequantize, for
+// gfx950.  Semantics follow the reference's torch implementation
+// (int4_triton/quantize.py:102-135) bit for bit; the kernel structure is this
+// library's own: one wave per (group, 64-column strip), min/max by wave
+// shuffles, nibble packing in registers and an LDS transpose so that every
+// qweight row segment is written as one coalesced 256-byte store.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+
+#include "w4_common.hpp"
+
+namespace w4 {
+
+__device__ __forceinline__ float max_nan(float a, float b) { return (a > b || a != a) ? a : b; }
+__device__ __forceinline__ float min_nan(float a, float b) { return (a < b || a != a) ? a : b; }
+// torch.clamp keeps NaN (quantize.py:108-113); fminf/fmaxf would drop it.
+__device__ __forceinline__ float clamp_nan(float x, float lo, float hi) {
+  return (x != x) ? x : fminf(fmaxf(x, lo), hi);
+}
+
+struct QStats {
+  float scale;  // fp16-representable (or 0/inf/NaN in degenerate groups)
+  float zero;
+};
+
+// quantize.py:108-112, in the same fp32 op order (true IEEE division).
+__device__ __forceinline__ QStats group_stats(float rmax, float rmin) {
+#pragma clang fp contract(off)
+  const float wmax = max_nan(rmax, 0.0f);
+  const float wmin = min_nan(rmin, 0.0f);
+  float scale = (wmax - wmin) / 15.0f;
+  if (scale == 0.0f) scale = 1.0f;
+  scale = (float)(_Float16)scale;
+  const float zero = clamp_nan(floorf(-wmin / scale + 0.5f), 0.0f, 15.0f);
+  QStats r;
+  r.scale = scale;
+  r.zero = zero;
+  return r;
+}
+
+// quantize.py:113-116: q = clamp(floor(w/scale + 0.5) + zero, 0, 15) -> int32
+// (NaN converts to INT32_MIN like the reference's CPU cast), packed with
+// int32 wrap-around.
+__device__ __forceinline__ uint32_t quantize_pack8(const float v[8], QStats st) {
+#pragma clang fp contract(off)
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float qf = clamp_nan(floorf(v[i] / st.scale + 0.5f) + st.zero, 0.0f, 15.0f);
+    const uint32_t q = (qf != qf) ? 0x80000000u : (uint32_t)(int)qf;
+    word += q << (4 * i);
+  }
+  return word;
+}
+
+// Stored fp16 patterns.  A NaN zero point is written as 0xFE00, the x86
+// "default NaN" that the reference's CPU path produces for -0/0 and for
+// negated NaN inputs; a NaN scale (NaN weights) as 0x7E00.
+__device__ __forceinline__ uint16_t scale_bits(float s) {
+  return (s != s) ? (uint16_t)0x7E00 : __builtin_bit_cast(uint16_t, (_Float16)s);
+}
+__device__ __forceinline__ uint16_t zero_bits(float z) {
+  return (z != z) ? (uint16_t)0xFE00 : __builtin_bit_cast(uint16_t, (_Float16)z);
+}
+
+template <int DT, bool VEC>
+__device__ __forceinline__ void load8(const uint16_t* __restrict__ w, int64_t n, int64_t k,
+                                      int64_t swn, int64_t swk, float v[8]) {
+  if (VEC) {
+    const u32x4 p = *reinterpret_cast<const u32x4*>(w + n * swn + k);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = act_bits_to_float((uint16_t)(p[i] & 0xFFFFu), DT);
+      v[2 * i + 1] = act_bits_to_float((uint16_t)(p[i] >> 16), DT);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = act_bits_to_float(w[n * swn + (k + i) * swk], DT);
+  }
+}
+
+constexpr int QROWS = 64;  // columns n per wave tile (= lanes, for the stores)
+constexpr int QWAVES = 4;  // independent wave tiles per workgroup
+
+// Single-pass kernel for G <= 512: lanes_per_row = G/8 lanes each own one
+// packed word of a row; 64/lanes_per_row rows are processed per iteration.
+template <int DT, int G, bool VEC>
+__global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
+    const uint16_t* __restrict__ w, int64_t N, int64_t K, int64_t swn, int64_t swk,
+    int32_t* __restrict__ qw, uint16_t* __restrict__ sc, uint16_t* __restrict__ ze,
+    int64_t tiles_n, int64_t tiles_total) {
+  constexpr int L = G / 8;            // lanes per row (4..64)
+  constexpr int RPI = 64 / L;         // rows per iteration
+  __shared__ uint32_t tile[QWAVES][L][QROWS + 1];
+  __shared__ uint16_t st_s[QWAVES][QROWS];
+  __shared__ uint16_t st_z[QWAVES][QROWS];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * QWAVES + wv;
+  const bool active = t < tiles_total;
+  const int64_t g = active ? t / tiles_n : 0;
+  const int64_t n0 = active ? (t % tiles_n) * QROWS : 0;
+  const int seg = lane % L;
+  const int rsub = lane / L;
+
+  if (active) {
+#pragma unroll 2
+    for (int it = 0; it < QROWS / RPI; ++it) {
+      const int row = it * RPI + rsub;
+      const int64_t n = n0 + row;
+      const bool valid = n < N;
+      float v[8];
+      if (valid) {
+        load8<DT, VEC>(w, n, g * G + seg * 8, swn, swk, v);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+      }
+      float mx = v[0], mn = v[0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) {
+        mx = max_nan(mx, v[i]);
+        mn = min_nan(mn, v[i]);
+      }
+#pragma unroll
+      for (int off = L / 2; off > 0; off >>= 1) {
+        mx = max_nan(mx, __shfl_xor(mx, off, 64));
+        mn = min_nan(mn, __shfl_xor(mn, off, 64));
+      }
+      const QStats st = group_stats(mx, mn);
+      tile[wv][seg][row] = quantize_pack8(v, st);
+      if (seg == 0) {
+        st_s[wv][row] = scale_bits(st.scale);
+        st_z[wv][row] = zero_bits(st.zero);
+      }
+    }
+  }
+  __syncthreads();
+  if (active) {
+    const int64_t n = n0 + lane;
+    if (n < N) {
+      const int64_t k8_0 = g * L;
+#pragma unroll 4
+      for (int kk = 0; kk < L; ++kk) qw[(k8_0 + kk) * N + n] = (int32_t)tile[wv][kk][lane];
+      sc[g * N + n] = st_s[wv][lane];
+      ze[g * N + n] = st_z[wv][lane];
+    }
+  }
+}
+
+// Two-pass kernel for G > 512 (per-channel G = K included): pass 1 reduces
+// min/max over the whole group row by row, pass 2 re-reads 512-wide chunks
+// and packs them.  One wave per (group, 64-column strip).
+template <int DT, bool VEC>
+__global__ __launch_bounds__(QWAVES * 64) void quantize_large_group_kernel(
+    const uint16_t* __restrict__ w, int64_t N, int64_t K, int64_t swn, int64_t swk, int G,
+    int32_t* __restrict__ qw, uint16_t* __restrict__ sc, uint16_t* __restrict__ ze,
+    int64_t tiles_n, int64_t tiles_total) {
+  __shared__ uint32_t tile[QWAVES][64][QROWS + 1];
+  __shared__ float st_scale[QWAVES][QROWS];
+  __shared__ float st_zero[QWAVES][QROWS];
+
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int64_t t = (int64_t)blockIdx.x * QWAVES + wv;
+  const bool active = t < tiles_total;
+  const int64_t g = active ? t / tiles_n : 0;
+  const int64_t n0 = active ? (t % tiles_n) * QROWS : 0;
+  const int nchunks = G / 512;
+
+  if (active) {
+    for (int row = 0; row < QROWS; ++row) {
+      const int64_t n = n0 + row;
+      if (n >= N) break;
+      float mx = 0.0f, mn = 0.0f;
+      bool first = true;
+      for (int c = 0; c < nchunks; ++c) {
+        float v[8];
+        load8<DT, VEC>(w, n, g * G + c * 512 + lane * 8, swn, swk, v);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          mx = first ? v[i] : max_nan(mx, v[i]);
+          mn = first ? v[i] : min_nan(mn, v[i]);
+          first = false;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) {
+        mx = max_nan(mx, __shfl_xor(mx, off, 64));
+        mn = min_nan(mn, __shfl_xor(mn, off, 64));
+      }
+      const QStats st = group_stats(mx, mn);
+      if (lane == 0) {
+        st_scale[wv][row] = st.scale;
+        st_zero[wv][row] = st.zero;
+      }
+    }
+  }
+  __syncthreads();
+  if (active) {
+    const int64_t n = n0 + lane;
+    if (n < N) {
+      sc[g * N + n] = scale_bits(st_scale[wv][lane]);
+      ze[g * N + n] = zero_bits(st_zero[wv][lane]);
+    }
+  }
+  for (int c = 0; c < nchunks; ++c) {
+    if (active) {
+      for (int row = 0; row < QROWS; ++row) {
+        const int64_t n = n0 + row;
+        if (n >= N) break;
+        float v[8];
+        load8<DT, VEC>(w, n, g * G + c * 512 + lane * 8, swn, swk, v);
+        QStats st;
+        st.scale = st_scale[wv][row];
+        st.zero = st_zero[wv][row];
+        tile[wv][lane][row] = quantize_pack8(v, st);
+      }
+    }
+    __syncthreads();
+    if (active) {
+      const int64_t n = n0 + lane;
+      if (n < N) {
+        const int64_t k8_0 = g * (G / 8) + (int64_t)c * 64;
+        for (int kk = 0; kk < 64; ++kk) qw[(k8_0 + kk) * N + n] = (int32_t)tile[wv][kk][lane];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// W_hat[N, K] = round_once((q - z) * s): 64x64-word tiles transposed through
+// LDS so that both the qweight reads and the W_hat row writes are coalesced.
+template <int ODT>
+__global__ __launch_bounds__(256) void dequantize_kernel(const int32_t* __restrict__ qw,
+                                                         const uint16_t* __restrict__ sc,
+                                                         const uint16_t* __restrict__ ze,
+                                                         int64_t N, int64_t K8, int gshift,
+                                                         void* __restrict__ out) {
+#pragma clang fp contract(off)
+  __shared__ uint32_t tile[64][65];
+  const int t = threadIdx.x;
+  const int64_t n0 = (int64_t)blockIdx.x * 64;
+  const int64_t k80 = (int64_t)blockIdx.y * 64;
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const int kk = i * 4 + (t >> 6), nn = t & 63;
+    const int64_t k8 = k80 + kk, n = n0 + nn;
+    tile[kk][nn] = (k8 < K8 && n < N) ? (uint32_t)qw[k8 * N + n] : 0u;
+  }
+  __syncthreads();
+  const int64_t K = K8 * 8;
+#pragma unroll 2
+  for (int i = 0; i < 16; ++i) {
+    const int nn = i * 4 + (t >> 6), kk = t & 63;
+    const int64_t k8 = k80 + kk, n = n0 + nn;
+    if (k8 >= K8 || n >= N) continue;
+    const uint32_t word = tile[kk][nn];
+    const int64_t g = (k8 * 8) >> gshift;
+    const float s = half_bits_to_float(sc[g * N + n]);
+    const float z = half_bits_to_float(ze[g * N + n]);
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      v[j] = ((float)((word >> (4 * j)) & 0xFu) - z) * s;
+      // Materialize the fp32 product: without this the backend folds
+      // multiply + fp16 cast into one mixed fma with a +0 addend, which
+      // turns a -0 product (q < z, s = 0) into +0.
+      asm volatile("" : "+v"(v[j]));
+    }
+    if constexpr (ODT == W4_DTYPE_FP32) {
+      float* o = reinterpret_cast<float*>(out) + n * K + k8 * 8;
+      f32x4 a, b;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        a[j] = v[j];
+        b[j] = v[4 + j];
+      }
+      *reinterpret_cast<f32x4*>(o) = a;
+      *reinterpret_cast<f32x4*>(o + 4) = b;
+    } else {
+      uint16_t* o = reinterpret_cast<uint16_t*>(out) + n * K + k8 * 8;
+      u32x4 p;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        p[j] = (uint32_t)float_to_act_bits<ODT>(v[2 * j]) |
+               ((uint32_t)float_to_act_bits<ODT>(v[2 * j + 1]) << 16);
+      *reinterpret_cast<u32x4*>(o) = p;
+    }
+  }
+}
+
+}  // namespace w4
+
+using namespace w4host;
+
+template <int DT, bool VEC>
+static void launch_quantize(const uint16_t* w, int64_t N, int64_t K, int64_t swn, int64_t swk,
+                            int G, int32_t* qw, uint16_t* sc, uint16_t* ze, hipStream_t st) {
+  const int64_t tiles_n = (N + w4::QROWS - 1) / w4::QROWS;
+  const int64_t tiles_total = tiles_n * (K / G);
+  const dim3 grid((unsigned)((tiles_total + w4::QWAVES - 1) / w4::QWAVES));
+  const dim3 block(w4::QWAVES * 64);
+#define W4_QS(GG)                                                                         \
+  case GG:                                                                                \
+    hipLaunchKernelGGL((w4::quantize_small_group_kernel<DT, GG, VEC>), grid, block, 0, st, \
+                       w, N, K, swn, swk, qw, sc, ze, tiles_n, tiles_total);              \
+    return;
+  switch (G) {
+    W4_QS(8)
+    W4_QS(16)
+    W4_QS(32)
+    W4_QS(64)
+    W4_QS(128)
+    W4_QS(256)
+    W4_QS(512)
+    default:
+      break;
+  }
+#undef W4_QS
+  hipLaunchKernelGGL((w4::quantize_large_group_kernel<DT, VEC>), grid, block, 0, st, w, N, K, swn,
+                     swk, G, qw, sc, ze, tiles_n, tiles_total);
+}
+
+extern "C" int w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K, int64_t stride_wn,
+                           int64_t stride_wk, int group_size, int32_t* qweight, uint16_t* scales,
+                           uint16_t* zeros, void* stream) {
+  clear_error();
+  if (w_dtype != W4_DTYPE_BF16 && w_dtype != W4_DTYPE_FP16)
+    return fail(W4_ERR_INVALID, "w4_quantize: weight dtype must be bf16 or fp16 (got code %d)", w_dtype);
+  if (N < 0 || K <= 0) return fail(W4_ERR_INVALID, "w4_quantize: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+  const int64_t G = group_size == -1 ? K : group_size;
+  if (G <= 0 || K % G != 0 || G % 8 != 0 || !is_pow2(G))
+    return fail(W4_ERR_INVALID,
+                "w4_quantize: group_size must be a power of two, a multiple of 8 and divide K "
+                "(K=%lld, group_size=%d)", (long long)K, group_size);
+  if (G > (int64_t)1 << 30) return fail(W4_ERR_UNSUPPORTED, "w4_quantize: group_size too large");
+  if (N == 0) return W4_OK;
+  if (!w || !qweight || !scales || !zeros) return fail(W4_ERR_INVALID, "w4_quantize: null pointer");
+  const uint16_t* wp = static_cast<const uint16_t*>(w);
+  const bool vec = stride_wk == 1 && (stride_wn % 8) == 0 && ((uintptr_t)wp % 16) == 0;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (w_dtype == W4_DTYPE_BF16) {
+    if (vec) launch_quantize<W4_DTYPE_BF16, true>(wp, N, K, stride_wn, stride_wk, (int)G, qweight, scales, zeros, st);
+    else launch_quantize<W4_DTYPE_BF16, false>(wp, N, K, stride_wn, stride_wk, (int)G, qweight, scales, zeros, st);
+  } else {
+    if (vec) launch_quantize<W4_DTYPE_FP16, true>(wp, N, K, stride_wn, stride_wk, (int)G, qweight, scales, zeros, st);
+    else launch_quantize<W4_DTYPE_FP16, false>(wp, N, K, stride_wn, stride_wk, (int)G, qweight, scales, zeros, st);
+  }
+  return check_launch("w4_quantize");
+}
+
+extern "C" int w4_dequantize(const int32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
+                             int64_t N, int64_t K, int group_size, int out_dtype, void* out,
+                             void* stream) {
+  clear_error();
+  if (N < 0 || K <= 0 || K % 8 != 0)
+    return fail(W4_ERR_INVALID, "w4_dequantize: bad shape N=%lld K=%lld", (long long)N, (long long)K);
+  const int64_t G = group_size == -1 ? K : group_size;
+  if (G <= 0 || K % G != 0 || G % 8 != 0 || !is_pow2(G))
+    return fail(W4_ERR_INVALID, "w4_dequantize: bad group_size %d for K=%lld", group_size, (long long)K);
+  if (N == 0) return W4_OK;
+  if (!qweight || !scales || !zeros || !out) return fail(W4_ERR_INVALID, "w4_dequantize: null pointer");
+  if (((uintptr_t)out % 16) != 0) return fail(W4_ERR_INVALID, "w4_dequantize: output must be 16-byte aligned");
+  const int64_t K8 = K / 8;
+  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)((K8 + 63) / 64));
+  const int gshift = ilog2(G);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (out_dtype) {
+    case W4_DTYPE_BF16:
+      hipLaunchKernelGGL((w4::dequantize_kernel<W4_DTYPE_BF16>), grid, dim3(256), 0, st, qweight, scales, zeros, N, K8, gshift, out);
+      break;
+    case W4_DTYPE_FP16:
+      hipLaunchKernelGGL((w4::dequantize_kernel<W4_DTYPE_FP16>), grid, dim3(256), 0, st, qweight, scales, zeros, N, K8, gshift, out);
+      break;
+    case W4_DTYPE_FP32:
+      hipLaunchKernelGGL((w4::dequantize_kernel<W4_DTYPE_FP32>), grid, dim3(256), 0, st, qweight, scales, zeros, N, K8, gshift, out);
+      break;
+    default:
+      return fail(W4_ERR_INVALID, "w4_dequantize: bad out dtype %d", out_dtype);
+  }
+  return check_launch("w4_dequantize");
+}

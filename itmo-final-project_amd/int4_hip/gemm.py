@@ -1,0 +1,114 @@
+"""Y = X @ W_hat^T with X in bf16/fp16 and W given as packed int4 (W4A16), on gfx950.
+
+Same public entry point, launch regimes and error behaviour as the reference
+(int4_triton/gemm.py:223-317):
+
+  * M == 1:        decode GEMV, one launch, no workspace;
+  * 2 <= M <= 64:  split-K with fp32 partials and a fixed-order reduce kernel;
+  * M > 64:        tiled MFMA GEMM writing the output dtype directly.
+
+The kernels are hand-written HIP (itmo-final-project_amd/csrc); the split
+counts come from a static table inside the library, so results are
+bit-identical from run to run and process to process (the reference picks its
+tiles by timing, gemm.py:161-168).  Every call launches on the caller's
+current stream and never synchronizes; the split-K workspace comes from
+torch's caching allocator, so calls can be captured in a CUDA/HIP graph.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+_XDT = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_FP16}
+SMALL_M = 64  # reference regime boundary (int4_triton/gemm.py:17)
+
+
+def _check_weight(qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, K: int):
+    assert qweight.dtype == torch.int32 and qweight.dim() == 2
+    assert scales.dtype == torch.float16 and zeros.dtype == torch.float16
+    assert scales.shape == zeros.shape and scales.shape[1] == qweight.shape[1]
+    G = K // scales.shape[0]
+    assert G * scales.shape[0] == K and G >= 8 and (G & (G - 1)) == 0, (K, scales.shape)
+    return G
+
+
+def w4a16_matmul(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor) -> torch.Tensor:
+    """x[..., K] (bf16/fp16) @ W^T, W given as packed int4 (see quantize.py). Returns x.dtype [..., N].
+
+    Mirrors int4_triton/gemm.py:303-309 (assertions included).
+    """
+    assert x.dtype in (torch.bfloat16, torch.float16)
+    K = x.shape[-1]
+    assert qweight.shape[0] * 8 == K, (qweight.shape, K)
+    G = _check_weight(qweight, scales, zeros, K)
+    assert x.is_cuda and qweight.device == x.device and scales.device == x.device and zeros.device == x.device
+    N = qweight.shape[1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    qweight, scales, zeros = qweight.contiguous(), scales.contiguous(), zeros.contiguous()
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    if M == 0 or N == 0:
+        return y.reshape(*x.shape[:-1], N)
+    lib = _lib.load()
+    ws_bytes = lib.w4a16_workspace_bytes(M, N, K, G)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    with torch.cuda.device(x.device):
+        rc = lib.w4a16_gemm(
+            x2.data_ptr(), _XDT[x.dtype], M, N, K, x2.stride(0), x2.stride(1),
+            qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(), G,
+            y.data_ptr(), N, ws.data_ptr() if ws is not None else None, ws_bytes,
+            torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(rc, "w4a16_gemm")
+    return y.reshape(*x.shape[:-1], N)
+
+
+def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
+                         out: Sequence[torch.Tensor] | None = None) -> list[torch.Tensor]:
+    """Several independent small-M products ``xs[i] @ W_i^T`` in ONE kernel launch.
+
+    ``weights[i]`` is a ``(qweight, scales, zeros)`` triple.  All ``xs[i]`` share
+    dtype and the leading size M (1 <= M <= 16).  This fuses the per-linear
+    decode launches of a transformer block (q/k/v, gate/up, ...); it has no
+    single counterpart in the reference.
+    """
+    assert 1 <= len(xs) == len(weights) <= _lib.MAX_GROUPED
+    dt = xs[0].dtype
+    assert dt in _XDT
+    dev = xs[0].device
+    M = xs[0].reshape(-1, xs[0].shape[-1]).shape[0]
+    assert 1 <= M <= 16
+    probs = (_lib.Problem * len(xs))()
+    outs, keep = [], []
+    for i, (x, (qw, s, z)) in enumerate(zip(xs, weights)):
+        assert x.dtype == dt and x.device == dev
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K).contiguous()
+        assert x2.shape[0] == M and qw.shape[0] * 8 == K
+        G = _check_weight(qw, s, z, K)
+        qw, s, z = qw.contiguous(), s.contiguous(), z.contiguous()
+        N = qw.shape[1]
+        y = out[i] if out is not None else torch.empty((M, N), dtype=dt, device=dev)
+        assert y.shape == (M, N) and y.is_contiguous() and y.dtype == dt
+        probs[i] = _lib.Problem(x2.data_ptr(), qw.data_ptr(), s.data_ptr(), z.data_ptr(), y.data_ptr(), N, K, G, 0)
+        keep += [x2, qw, s, z]
+        outs.append(y)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.w4a16_gemm_grouped(probs, len(xs), _XDT[dt], M, torch.cuda.current_stream(dev).cuda_stream)
+    _lib.check(rc, "w4a16_gemm_grouped")
+    return [y.reshape(*x.shape[:-1], y.shape[-1]) for x, y in zip(xs, outs)]
+
+
+def w16a16_matmul(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x[..., K] @ w[N, K]^T with full-precision weights (the reference's W16 baseline,
+    int4_triton/gemm.py:312-317).
+
+    On MI355X this baseline is the vendor library (hipBLASLt through
+    ``F.linear``); no hand-written kernel is provided for it.
+    """
+    assert x.dtype == w.dtype and x.dtype in (torch.bfloat16, torch.float16)
+    return F.linear(x, w)

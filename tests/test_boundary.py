@@ -1,0 +1,135 @@
+"""CPU tests of the drop-in boundary: the C-ABI library, argument validation
+(C side and Python side, mirroring the reference's assertions), module
+structure.  No GPU compute is issued here."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+import torch.nn as nn
+
+import int4_hip
+from int4_hip import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "int4_hip.h"
+
+
+def _header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\**\s+\**(w4[a-z0-9_]*)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_expected_entry_points():
+    assert _header_functions() == sorted(_lib.SIGNATURES)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} is not built (run __graft_entry__.build())")
+    return _lib.load()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _header_functions():
+        assert hasattr(lib, name), name
+    assert lib.w4_abi_version() == _lib.ABI_VERSION
+
+
+def test_c_abi_rejects_bad_quantize_arguments(lib):
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    # bad dtype
+    assert lib.w4_quantize(fake, 7, 4, 64, 64, 1, 32, fake, fake, fake, None) == _lib.ERR_INVALID
+    assert b"dtype" in lib.w4_last_error()
+    # group size not a power of two / not dividing K / not a multiple of 8
+    for g in (24, 48, 12, 3):
+        assert lib.w4_quantize(fake, 0, 4, 96, 96, 1, g, fake, fake, fake, None) == _lib.ERR_INVALID
+    # per-channel with non power-of-two K (the reference asserts the same)
+    assert lib.w4_quantize(fake, 0, 4, 96, 96, 1, -1, fake, fake, fake, None) == _lib.ERR_INVALID
+    # null pointers
+    assert lib.w4_quantize(None, 0, 4, 64, 64, 1, 32, fake, fake, fake, None) == _lib.ERR_INVALID
+    # empty N is a no-op success
+    assert lib.w4_quantize(None, 0, 0, 64, 64, 1, 32, None, None, None, None) == _lib.OK
+
+
+def test_c_abi_rejects_bad_gemm_arguments(lib):
+    fake = ctypes.c_void_p(16)
+    args = dict(x=fake, dt=0, M=1, N=8, K=64, sxm=64, sxk=1, qw=fake, s=fake, z=fake, G=32, y=fake, ldy=8)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.w4a16_gemm(a["x"], a["dt"], a["M"], a["N"], a["K"], a["sxm"], a["sxk"], a["qw"], a["s"],
+                              a["z"], a["G"], a["y"], a["ldy"], None, 0, None)
+
+    assert call(dt=2) == _lib.ERR_INVALID          # fp32 activations are not supported
+    assert call(K=60) == _lib.ERR_INVALID          # K % 8
+    assert call(G=48) == _lib.ERR_INVALID          # not a power of two
+    assert call(G=128) == _lib.ERR_INVALID         # does not divide K
+    assert call(ldy=4) == _lib.ERR_INVALID         # ldy < N
+    assert call(x=None) == _lib.ERR_INVALID
+    assert call(M=0) == _lib.OK                    # empty product
+    assert lib.w4a16_workspace_bytes(65, 4096, 4096, 128) == 0  # M > 64: no split-K
+
+
+def test_c_abi_rejects_bad_grouped_arguments(lib):
+    probs = (_lib.Problem * 1)()
+    assert lib.w4a16_gemm_grouped(probs, 0, 0, 1, None) == _lib.ERR_INVALID
+    assert lib.w4a16_gemm_grouped(probs, 1, 0, 17, None) == _lib.ERR_INVALID
+    assert lib.w4a16_gemm_grouped(probs, 1, 0, 1, None) == _lib.ERR_INVALID  # null pointers
+    assert lib.w4a16_gemm_grouped(probs, _lib.MAX_GROUPED + 1, 0, 1, None) == _lib.ERR_INVALID
+
+
+# ---------------------------------------------------------- Python-side asserts
+# Same exception type as the reference (AssertionError) for the same misuse
+# (int4_triton/quantize.py:69-75, int4_triton/gemm.py:305-307, qlinear.py:13).
+def test_quantize_asserts_like_reference():
+    w = torch.zeros(16, 64, dtype=torch.bfloat16)
+    with pytest.raises(AssertionError):
+        int4_hip.quantize_int4(w)  # not on the GPU
+    with pytest.raises(AssertionError):
+        int4_hip.quantize_int4(torch.zeros(16, 64, 2, dtype=torch.bfloat16))
+
+
+def test_matmul_asserts_like_reference():
+    qw = torch.zeros(8, 16, dtype=torch.int32)
+    s = torch.ones(2, 16, dtype=torch.float16)
+    with pytest.raises(AssertionError):
+        int4_hip.w4a16_matmul(torch.zeros(1, 64, dtype=torch.float32), qw, s, s)
+    with pytest.raises(AssertionError):
+        int4_hip.w4a16_matmul(torch.zeros(1, 72, dtype=torch.bfloat16), qw, s, s)  # K != 8*qweight rows
+
+
+def test_int4linear_buffers_match_reference_layout():
+    m = int4_hip.Int4Linear(256, 48, group_size=64, bias=True, device="cpu")
+    sd = m.state_dict()
+    assert list(sd) == ["qweight", "scales", "zeros", "bias"]
+    assert sd["qweight"].shape == (32, 48) and sd["qweight"].dtype == torch.int32
+    assert sd["scales"].shape == (4, 48) and sd["scales"].dtype == torch.float16
+    assert sd["zeros"].shape == (4, 48) and sd["zeros"].dtype == torch.float16
+    assert "group_size=64" in repr(m)
+    with pytest.raises(AssertionError):
+        int4_hip.Int4Linear(100, 8, group_size=64)
+
+
+def test_iter_linears_skip_rule():
+    from int4_hip.qlinear import _iter_linears
+
+    model = nn.Sequential()
+    model.add_module("block", nn.Sequential(nn.Linear(8, 8), nn.ReLU(), nn.Linear(8, 8)))
+    model.add_module("lm_head", nn.Linear(8, 4))
+    names = [n for _, n, _ in _iter_linears(model, ("lm_head",))]
+    assert names == ["0", "2"]
+    assert len(list(_iter_linears(model, ()))) == 3
+
+
+def test_product_package_does_not_import_the_oracle():
+    pkg = ROOT / "itmo-final-project_amd"
+    for p in list(pkg.rglob("*.py")) + list(pkg.rglob("*.hip")) + list(pkg.rglob("*.cpp")):
+        assert "oracle" not in p.read_text(), f"{p} references the test oracle"
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.load(tmp_path / "nope.so")

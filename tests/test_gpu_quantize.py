@@ -1,0 +1,125 @@
+"""GPU parity: the HIP quantize/pack and dequantize kernels against the CPU
+oracle (bit-exact) and the reference's golden vectors."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import int4_hip
+from oracle import w4a16_oracle as O
+from golden.make_golden import sha, synth_weight_bits
+from _synth import assert_bits_equal_nan_aware, bits_of, randn
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+GOLDEN = Path(__file__).resolve().parent / "golden"
+_G = np.load(GOLDEN / "quantize_golden.npz")
+CASES = sorted({k.split("__")[0] for k in _G.files})
+LLAMA = [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192)]
+TDT = {"bf16": torch.bfloat16, "fp16": torch.float16}
+
+
+def _to_dev(bits: np.ndarray, dt: str) -> torch.Tensor:
+    return torch.from_numpy(bits.view(np.int16).copy()).view(TDT[dt]).to(DEV)
+
+
+def _quantize_np(w: torch.Tensor, g: int):
+    qw, s, z = int4_hip.quantize_int4(w, g)
+    torch.cuda.synchronize()
+    return qw.cpu().numpy(), bits_of(s), bits_of(z)
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_quantize_golden_bit_exact(name):
+    g, dt = _G[name + "__meta"]
+    dt = "bf16" if dt == 0 else "fp16"
+    print(f"[quantize golden] {name}", flush=True)
+    qw, s, z = _quantize_np(_to_dev(_G[name + "__w"], dt), int(g))
+    np.testing.assert_array_equal(qw, _G[name + "__qweight"])
+    np.testing.assert_array_equal(s, _G[name + "__scales"])
+    np.testing.assert_array_equal(z, _G[name + "__zeros"])
+
+
+def test_quantize_golden_hashes_large():
+    meta = json.loads((GOLDEN / "quantize_golden_hashes.json").read_text())
+    for c in meta["cases"]:
+        print(f"[quantize hash] {c['n']}x{c['k']} G={c['group_size']} {c['dtype']}", flush=True)
+        bits = synth_weight_bits(c["n"], c["k"], c["seed"], c["dtype"], c["sigma"])
+        qw, s, z = _quantize_np(_to_dev(bits, c["dtype"]), c["group_size"])
+        assert sha(qw) == c["qweight_sha256"], c
+        assert sha(s) == c["scales_sha256"], c
+        assert sha(z) == c["zeros_sha256"], c
+
+
+QCASES = ([(shape, g) for shape in LLAMA[:3] for g in (32, 128, -1)]
+          + [((2048, 2048), g) for g in (8, 16, 64, 256, 512, 1024)]
+          + [((100, 256), g) for g in (8, 32, 64, 128, 256, -1)]
+          + [((73, 1024), g) for g in (16, 128, 1024)])
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("shape,g", QCASES)
+def test_quantize_matches_oracle(shape, g, dt):
+    N, K = shape
+    print(f"[quantize] {shape} G={g} {dt}", flush=True)
+    w = randn(shape, seed=N + K + max(g, 0), sigma=0.02, dtype=TDT[dt])
+    qw, s, z = _quantize_np(w.to(DEV), g)
+    rq, rs, rz = O.quantize_int4(bits_of(w), dt, g)
+    np.testing.assert_array_equal(qw, rq)
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(z, rz)
+
+
+@pytest.mark.parametrize("layout", ["transposed", "sliced", "unaligned"])
+def test_quantize_strided_input(layout):
+    base = randn((512, 640), seed=3, sigma=0.02)
+    views = {
+        "transposed": lambda b: b.t(),              # [640, 512], stride_wk = 640
+        "sliced": lambda b: b[:, 64:576],           # row stride 640, 16-byte aligned
+        "unaligned": lambda b: b[:, 3:515],         # row stride 640, 6-byte offset
+    }
+    w = views[layout](base)
+    assert not w.is_contiguous()
+    qw, s, z = _quantize_np(views[layout](base.to(DEV)), 128)
+    rq, rs, rz = O.quantize_int4(bits_of(w.contiguous()), "bf16", 128)
+    np.testing.assert_array_equal(qw, rq)
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(z, rz)
+
+
+def test_memory_reduction_and_error():
+    # int4_triton tests/test_kernels.py:34-44
+    N, K = 2048, 8192
+    w = (randn((N, K), seed=0, sigma=0.02, dtype=torch.float32)).half().to(DEV)
+    qw, s, z = int4_hip.quantize_int4(w, 128)
+    assert qw.dtype == torch.int32 and qw.shape == (K // 8, N)
+    assert w.numel() * w.element_size() == 4 * qw.numel() * qw.element_size()
+    w_hat = int4_hip.dequantize_int4(qw, s, z)
+    step = s.t().repeat_interleave(128, dim=1).float()
+    assert ((w_hat.float() - w.float()).abs() <= step * 0.5 + 1e-3).all()
+
+
+@pytest.mark.parametrize("odt", ["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("name", CASES)
+def test_dequantize_golden(name, odt):
+    g, dt = _G[name + "__meta"]
+    qw = torch.from_numpy(_G[name + "__qweight"]).to(DEV)
+    s = _to_dev(_G[name + "__scales"], "fp16")
+    z = _to_dev(_G[name + "__zeros"], "fp16")
+    tdt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[odt]
+    out = int4_hip.dequantize_int4(qw, s, z, tdt).cpu()
+    if odt == "fp32":
+        assert_bits_equal_nan_aware(out.numpy().view(np.uint32), _G[name + "__deq_fp32"].view(np.uint32), "fp32", name)
+    else:
+        assert_bits_equal_nan_aware(bits_of(out), _G[name + "__deq_" + odt], odt, name)
+
+
+@pytest.mark.parametrize("g", [32, 128])
+def test_dequantize_matches_oracle_large(g):
+    w = randn((2048, 2048), seed=5, sigma=0.02)
+    qw, s, z = int4_hip.quantize_int4(w.to(DEV), g)
+    out = int4_hip.dequantize_int4(qw, s, z, torch.bfloat16).cpu()
+    ref = O.f32_to_bf16_bits(O.dequantize_int4(qw.cpu().numpy(), bits_of(s), bits_of(z), "bf16"))
+    np.testing.assert_array_equal(bits_of(out), ref)
