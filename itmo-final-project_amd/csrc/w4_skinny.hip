@@ -387,7 +387,10 @@ void launch_skinny_mb(int mb, dim3 grid, dim3 block, size_t lds, hipStream_t st,
 
 }  // namespace
 
-// Called by w4a16_gemm for 1 <= M <= 64 (validation already done there).
+int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_dtype, void* y, int64_t ldy,
+                            hipStream_t st);
+
+// Called by w4a16_gemm for 17 <= M <= 64 (validation already done there).
 size_t w4_skinny_workspace_bytes(int64_t M, int64_t N, int64_t K, bool vec4_ok) {
   return plan_skinny(M, N, K, vec4_ok).ws_bytes;
 }
@@ -434,38 +437,32 @@ int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K
   }
   int rc = check_launch("w4a16_gemm (skinny)");
   if (rc != W4_OK || p.splits == 1) return rc;
+  return w4_splitk_reduce_launch(static_cast<const float*>(ws), (int)p.splits, M, N, x_dtype, y, ldy, st);
+}
+
+int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_dtype, void* y, int64_t ldy,
+                            hipStream_t st) {
   const int64_t MN = M * N;
   const dim3 rgrid((unsigned)((MN + 255) / 256));
   if (x_dtype == W4_DTYPE_BF16)
-    hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_BF16>), rgrid, dim3(256), 0, st,
-                       static_cast<const float*>(ws), (int)p.splits, M, N, static_cast<uint16_t*>(y), ldy);
+    hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_BF16>), rgrid, dim3(256), 0, st, ws, S, M, N,
+                       static_cast<uint16_t*>(y), ldy);
   else
-    hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_FP16>), rgrid, dim3(256), 0, st,
-                       static_cast<const float*>(ws), (int)p.splits, M, N, static_cast<uint16_t*>(y), ldy);
+    hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_FP16>), rgrid, dim3(256), 0, st, ws, S, M, N,
+                       static_cast<uint16_t*>(y), ldy);
   return check_launch("w4a16_gemm (split-K reduce)");
 }
 
-extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
-                                  void* stream) {
-  clear_error();
-  if (count < 1 || count > W4_MAX_GROUPED)
-    return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: count must be in [1, %d]", W4_MAX_GROUPED);
-  if (!problems) return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: null problem list");
-  if (x_dtype != W4_DTYPE_BF16 && x_dtype != W4_DTYPE_FP16)
-    return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: x dtype must be bf16 or fp16");
-  if (M < 1 || M > 16) return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: M must be in [1, 16]");
+// Grouped launch with activations read from global memory (no LDS staging):
+// used when the decode kernel's staged rows would not fit in LDS.
+int w4_skinny_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M, hipStream_t st) {
   w4::GroupedArgs g{};
   g.count = count;
   int64_t tiles = 0;
   const int nw = 8;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
-    if (!q.x || !q.qweight || !q.scales || !q.zeros || !q.y)
-      return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: null pointer in problem %d", i);
     const int64_t G = q.group_size;
-    if (q.N < 1 || q.K < 8 || q.K % 8 != 0 || G < 8 || !is_pow2(G) || q.K % G != 0)
-      return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: bad shape in problem %d (N=%lld K=%lld G=%d)", i,
-                  (long long)q.N, (long long)q.K, q.group_size);
     w4::SkinnyArgs& a = g.prob[i];
     a.x = static_cast<const uint16_t*>(q.x);
     a.sxm = q.K;
@@ -493,7 +490,6 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
   }
   for (int i = count; i <= W4_MAX_GROUPED; ++i) g.tile_start[i] = tiles;
   const size_t lds = (size_t)nw * (size_t)M * 64 * sizeof(float);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   if (x_dtype == W4_DTYPE_BF16)
     hipLaunchKernelGGL((w4::grouped_kernel<W4_DTYPE_BF16, 1>), dim3((unsigned)tiles), dim3(nw * 64), lds, st, g);
   else
