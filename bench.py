@@ -145,7 +145,13 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-passes", type=int, default=5)
+    ap.add_argument("--only", default="all",
+                    help="comma list of sections to run: decode, perlinear, splitk, prefill, quantize "
+                         "(profiling runs use one section; the JSON line needs 'decode')")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run one 32 MiB device copy (for scaling FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
+    only = set(args.only.split(",")) if args.only != "all" else {"decode", "perlinear", "splitk", "prefill", "quantize"}
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the W4A16 path has no collective); "
               "run with --gpus 1", file=sys.stderr)
@@ -172,14 +178,24 @@ def main() -> int:
     ys1 = [[torch.empty((1, N), device=dev, dtype=torch.bfloat16) for _, N, K in LINEARS] for _ in range(nsets)]
     torch.cuda.synchronize()
 
-    # ------------------------------------------------- quantize kernel (load time)
-    def quant_set(i):
-        return lambda: [int4_hip.quantize_int4(w, G) for w in w16[i]]
+    if args.copy_calib:
+        src = torch.empty(32 << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
-    gq = graph_of(lambda: [quant_set(i)() for i in range(nsets)], stream)
-    q_ms = time_graph(gq, 3, stream) / nsets
+    # ------------------------------------------------- quantize kernel (load time)
+    q_ms = None
     q_bytes = sum(2 * N * K + N * K // 2 + 4 * N * K // G for _, N, K in LINEARS)
-    del gq
+    if "quantize" in only:
+        def quant_set(i):
+            return lambda: [int4_hip.quantize_int4(w, G) for w in w16[i]]
+
+        gq = graph_of(lambda: [quant_set(i)() for i in range(nsets)], stream)
+        q_ms = time_graph(gq, 3, stream) / nsets
+        del gq
     del w16
     torch.cuda.empty_cache()
 
@@ -189,59 +205,69 @@ def main() -> int:
 
     steps = max(nsets, (args.steps + nsets - 1) // nsets * nsets)
     warm = max(1, args.warmup // nsets)
-    g_main = graph_of(lambda: [grouped(i)() for i in range(nsets)], stream)
-    time_graph(g_main, warm, stream)
-    ms_rot = time_graph(g_main, steps // nsets, stream)
-    ms_per_step = ms_rot / nsets
     bytes1 = block_bytes(1)
-    value = bytes1 / (ms_per_step * 1e-3) / 1e9
-    kern_ms = per_launch_ms([grouped(i) for i in range(nsets)], stream)
-    kern_ms_src = "hip-events-around-each-launch-in-graph"
-    if kern_ms is None:
-        kern_ms, kern_ms_src = ms_per_step, "graph-replay-average"
-    achieved = bytes1 / (kern_ms * 1e-3) / 1e9
+    ms_per_step = kern_ms = value = achieved = None
+    kern_ms_src = None
+    if "decode" in only:
+        g_main = graph_of(lambda: [grouped(i)() for i in range(nsets)], stream)
+        time_graph(g_main, warm, stream)
+        ms_rot = time_graph(g_main, steps // nsets, stream)
+        ms_per_step = ms_rot / nsets
+        value = bytes1 / (ms_per_step * 1e-3) / 1e9
+        kern_ms = per_launch_ms([grouped(i) for i in range(nsets)], stream)
+        kern_ms_src = "hip-events-around-each-launch-in-graph"
+        if kern_ms is None:
+            kern_ms, kern_ms_src = ms_per_step, "graph-replay-average (16 launches per replay)"
+        achieved = bytes1 / (kern_ms * 1e-3) / 1e9
+        del g_main
 
     # ------------------------------------------------- M=1 per-linear launches (reference-comparable)
     def single(i, j):
         return lambda: int4_hip.w4a16_matmul(xs1[i][j], *packed[i][j])
 
-    per_lin = {}
-    for j, (name, N, K) in enumerate(LINEARS):
-        gj = graph_of(lambda j=j: [single(i, j)() for i in range(nsets)], stream)
-        time_graph(gj, 2, stream)
-        per_lin[name] = time_graph(gj, 10, stream) / nsets * 1e3
-        del gj
-    g7 = graph_of(lambda: [single(i, j)() for i in range(nsets) for j in range(len(LINEARS))], stream)
-    time_graph(g7, 2, stream)
-    ms7 = time_graph(g7, 10, stream) / nsets
-    del g7
+    per_lin, ms7 = {}, None
+    if "perlinear" in only:
+        for j, (name, N, K) in enumerate(LINEARS):
+            gj = graph_of(lambda j=j: [single(i, j)() for i in range(nsets)], stream)
+            time_graph(gj, 2, stream)
+            per_lin[name] = time_graph(gj, 10, stream) / nsets * 1e3
+            del gj
+        g7 = graph_of(lambda: [single(i, j)() for i in range(nsets) for j in range(len(LINEARS))], stream)
+        time_graph(g7, 2, stream)
+        ms7 = time_graph(g7, 10, stream) / nsets
+        del g7
 
     # ------------------------------------------------- split-K M=16 block
-    xs16 = [torch.randn((16, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
-    g16 = graph_of(lambda: [int4_hip.w4a16_matmul(xs16[j], *packed[i][j]) for i in range(nsets)
-                            for j in range(len(LINEARS))], stream)
-    time_graph(g16, 2, stream)
-    ms16 = time_graph(g16, 5, stream) / nsets
-    del g16
+    ms16 = None
+    if "splitk" in only:
+        xs16 = [torch.randn((16, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
+        g16 = graph_of(lambda: [int4_hip.w4a16_matmul(xs16[j], *packed[i][j]) for i in range(nsets)
+                                for j in range(len(LINEARS))], stream)
+        time_graph(g16, 2, stream)
+        ms16 = time_graph(g16, 5, stream) / nsets
+        del g16
 
-    # ------------------------------------------------- prefill M=2048
+    # ------------------------------------------------- prefill M=128/512/2048
     pre = {}
-    for M in (128, 512, 2048):
-        xsM = [torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
-        gp = graph_of(lambda: [int4_hip.w4a16_matmul(xsM[j], *packed[0][j]) for j in range(len(LINEARS))], stream)
-        time_graph(gp, 3, stream)
-        msM = time_graph(gp, 10, stream)
-        pre[M] = {"us_per_block": round(msM * 1e3, 2), "tflops": round(block_flops(M) / (msM * 1e-3) / 1e12, 2)}
-        del gp
-        if M == 2048:
-            w_deq = [int4_hip.dequantize_int4(*packed[0][j], torch.bfloat16) for j in range(len(LINEARS))]
-            gb = graph_of(lambda: [torch.nn.functional.linear(xsM[j], w_deq[j]) for j in range(len(LINEARS))], stream)
-            time_graph(gb, 3, stream)
-            msb = time_graph(gb, 10, stream)
-            pre[M]["hipblaslt_bf16_dequantized_us"] = round(msb * 1e3, 2)
-            pre[M]["hipblaslt_bf16_tflops"] = round(block_flops(M) / (msb * 1e-3) / 1e12, 2)
-            del gb, w_deq
-        del xsM
+    if "prefill" in only:
+        for M in (128, 512, 2048):
+            xsM = [torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
+            gp = graph_of(lambda: [int4_hip.w4a16_matmul(xsM[j], *packed[0][j]) for j in range(len(LINEARS))],
+                          stream)
+            time_graph(gp, 3, stream)
+            msM = time_graph(gp, 10, stream)
+            pre[M] = {"us_per_block": round(msM * 1e3, 2), "tflops": round(block_flops(M) / (msM * 1e-3) / 1e12, 2)}
+            del gp
+            if M == 2048:
+                w_deq = [int4_hip.dequantize_int4(*packed[0][j], torch.bfloat16) for j in range(len(LINEARS))]
+                gb = graph_of(lambda: [torch.nn.functional.linear(xsM[j], w_deq[j]) for j in range(len(LINEARS))],
+                              stream)
+                time_graph(gb, 3, stream)
+                msb = time_graph(gb, 10, stream)
+                pre[M]["hipblaslt_bf16_dequantized_us"] = round(msb * 1e3, 2)
+                pre[M]["hipblaslt_bf16_tflops"] = round(block_flops(M) / (msb * 1e-3) / 1e12, 2)
+                del gb, w_deq
+            del xsM
     torch.cuda.synchronize()
 
     # ------------------------------------------------- CPU baseline (rank 0, N=1)
@@ -254,13 +280,13 @@ def main() -> int:
 
     out = {
         "metric": METRIC,
-        "value": round(value, 2),
+        "value": round(value, 2) if value is not None else None,
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warm * nsets,
-        "ms_per_step": round(ms_per_step, 6),
-        "us_per_block": round(ms_per_step * 1e3, 3),
+        "ms_per_step": round(ms_per_step, 6) if ms_per_step is not None else None,
+        "us_per_block": round(ms_per_step * 1e3, 3) if ms_per_step is not None else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -270,21 +296,22 @@ def main() -> int:
                                "decode GEMV as one grouped launch, G=128, bf16 activations, "
                                f"{nsets} rotated weight sets ({nsets * bytes1 / 1e6:.0f} MB)",
                    "M": 1, "group_size": G, "weight_sets": nsets, "bytes_per_step": bytes1},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "w4::grouped_kernel<bf16>", "kernel_us": round(kern_ms * 1e3, 3),
-                     "kernel_time_source": kern_ms_src},
+        "roofline": None if achieved is None else {
+            "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "w4::gemv_grouped_kernel<0>", "kernel_us": round(kern_ms * 1e3, 3),
+            "kernel_time_source": kern_ms_src},
         "cpu_baseline": cpu,
         "decode_m1_per_linear_us": {k: round(v, 3) for k, v in per_lin.items()},
-        "decode_m1_7_launches_us_per_block": round(ms7 * 1e3, 3),
-        "decode_m1_7_launches_gbps": round(bytes1 / (ms7 * 1e-3) / 1e9, 1),
-        "splitk_m16_us_per_block": round(ms16 * 1e3, 3),
-        "splitk_m16_gbps": round(block_bytes(16) / (ms16 * 1e-3) / 1e9, 1),
+        "decode_m1_7_launches_us_per_block": round(ms7 * 1e3, 3) if ms7 else None,
+        "decode_m1_7_launches_gbps": round(bytes1 / (ms7 * 1e-3) / 1e9, 1) if ms7 else None,
+        "splitk_m16_us_per_block": round(ms16 * 1e3, 3) if ms16 else None,
+        "splitk_m16_gbps": round(block_bytes(16) / (ms16 * 1e-3) / 1e9, 1) if ms16 else None,
         "prefill": {str(k): v for k, v in pre.items()},
-        "prefill_m2048_tflops": pre[2048]["tflops"],
-        "prefill_m2048_mfma_frac": round(pre[2048]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4),
-        "quantize_us_per_block": round(q_ms * 1e3, 2),
-        "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1),
+        "prefill_m2048_tflops": pre[2048]["tflops"] if pre else None,
+        "prefill_m2048_mfma_frac": round(pre[2048]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4) if pre else None,
+        "quantize_us_per_block": round(q_ms * 1e3, 2) if q_ms else None,
+        "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None,
         "device": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(out), flush=True)

@@ -39,6 +39,11 @@ extern "C" {
 #define W4_DTYPE_FP16 1
 #define W4_DTYPE_FP32 2
 
+/* Every workspace starts with this many bytes of per-tile arrival counters:
+ * zero before the first call that uses the workspace, left zero by every call.
+ * The rest is scratch (fp32 partial sums). */
+#define W4_WORKSPACE_COUNTER_BYTES 65536
+
 /* status codes */
 #define W4_OK 0
 #define W4_ERR_INVALID 1     /* bad shape, stride, dtype or group size       */
@@ -79,7 +84,11 @@ int w4_dequantize(const int32_t* qweight, const uint16_t* scales, const uint16_t
  * Bytes of workspace w4a16_gemm needs for this problem (0 when the chosen
  * launch writes y directly).  Depends only on (M, N, K, group_size) and the
  * device's compute-unit count, never on timing, so the split-K decomposition
- * (and therefore every output bit) is the same in every process.
+ * (and therefore every output bit) is the same in every process.  The
+ * workspace (256-byte aligned) starts with the W4_WORKSPACE_COUNTER_BYTES
+ * counter area, so one zero-filled buffer of the largest size needed can be
+ * reused by all calls (w4a16_gemm and w4a16_gemm_grouped) issued on one
+ * stream.
  * Replaces: the per-call `partials` allocation, int4_triton/gemm.py:268.
  */
 size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
@@ -89,9 +98,10 @@ size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
  * accumulation, y in x's dtype.  x: bf16/fp16, any strides (stride_xm,
  * stride_xk).  qweight/scales/zeros dense row-major as above.  y: row stride
  * ldy (>= N), unit column stride.  Launch regimes (same boundaries as the
- * reference): M == 1 decode GEMV; 2 <= M <= 64 split-K with fp32 partials in
- * `workspace` and a fixed-order reduce (bit-identical run to run); M > 64
- * tiled MFMA GEMM.
+ * reference): M == 1 decode GEMV in one launch (long K split over workgroups,
+ * finished by the last one in split order); 2 <= M <= 64 split-K with fp32
+ * partials in `workspace` and a fixed-order reduce kernel; M > 64 tiled MFMA
+ * GEMM.  Every regime is bit-identical run to run.
  * Replaces: int4_triton/gemm.py:303-309 (w4a16_matmul) and its dispatcher
  * _matmul, :234-300 (kernels :74-157, :171-182, :185-220).
  */
@@ -120,17 +130,24 @@ typedef struct w4a16_problem {
 #define W4_MAX_GROUPED 8
 
 /*
+ * Bytes of workspace w4a16_gemm_grouped needs for these problems (0 if none).
+ */
+size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, int64_t M);
+
+/*
  * Up to W4_MAX_GROUPED independent small-M (1 <= M <= 16) products in ONE
- * kernel launch, all with the same activation dtype and M.  Each output
- * column's reduction over K stays inside one workgroup (no workspace, no
- * atomics), so results are bit-identical to w4a16_gemm's direct path only up
- * to summation order, and bit-identical run to run.
+ * kernel launch, all with the same activation dtype and M.  Problems with a
+ * long K are split over several workgroups whose fp32 partials are summed, in
+ * split order, by the last workgroup of each column tile to finish; that needs
+ * `workspace` (256-byte aligned, w4a16_grouped_workspace_bytes long, laid out
+ * like w4a16_gemm's).  Reusing one workspace for calls that run concurrently
+ * (on different streams) is a race.  Results are bit-identical run to run.
  * No single counterpart in the reference: it fuses the per-linear launches of
  * int4_triton/gemm.py:245-264 that a decoder block issues back to back
  * (q/k/v/o/gate/up/down, benchmarks/bench_gemm.py:18-26).
  */
 int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
-                       void* stream);
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

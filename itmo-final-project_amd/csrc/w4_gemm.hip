@@ -14,9 +14,10 @@ int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K
 size_t w4_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int G);
 int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
                    const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, void* y, int64_t ldy,
-                   void* ws, size_t ws_bytes, hipStream_t st);
-int w4_gemv_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M, hipStream_t st);
-int w4_skinny_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M, hipStream_t st);
+                   unsigned* counters, void* ws, size_t ws_bytes, hipStream_t st);
+int w4_gemv_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
+                           unsigned* counters, void* scratch, size_t scratch_bytes, hipStream_t st);
+int64_t w4_gemv_grouped_scratch_bytes(const w4a16_problem* problems, int count, int64_t M);
 int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
                       void* y, int64_t ldy, hipStream_t st);
@@ -26,13 +27,32 @@ static constexpr int64_t kSmallM = 64;
 // Decode-shaped products (activations staged in LDS) up to this M.
 static constexpr int64_t kDecodeM = 16;
 
+// Every workspace starts with a W4_WORKSPACE_COUNTER_BYTES area of per-tile
+// arrival counters (zero before first use, left zero by every call), then
+// scratch (fp32 partial sums).
 extern "C" size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size) {
   if (M < 1 || M > kSmallM || N < 1 || K < 8 || group_size < 8) return 0;
-  if (M <= kDecodeM) return w4_gemv_workspace_bytes(M, N, K, group_size);
-  // Sized for the 16-byte-aligned layout (the larger of the two plans).
-  const size_t a = w4_skinny_workspace_bytes(M, N, K, (N % 4) == 0);
-  const size_t b = w4_skinny_workspace_bytes(M, N, K, false);
-  return a > b ? a : b;
+  size_t scratch;
+  if (M <= kDecodeM) {
+    scratch = w4_gemv_workspace_bytes(M, N, K, group_size);
+  } else {
+    const size_t a = w4_skinny_workspace_bytes(M, N, K, (N % 4) == 0);
+    const size_t b = w4_skinny_workspace_bytes(M, N, K, false);
+    scratch = a > b ? a : b;
+  }
+  return scratch > 0 ? W4_WORKSPACE_COUNTER_BYTES + scratch : 0;
+}
+
+static void split_workspace(void* ws, size_t ws_bytes, unsigned** counters, void** scratch, size_t* scratch_bytes) {
+  if (ws == nullptr || ws_bytes < W4_WORKSPACE_COUNTER_BYTES || ((uintptr_t)ws % 256) != 0) {
+    *counters = nullptr;
+    *scratch = nullptr;
+    *scratch_bytes = 0;
+    return;
+  }
+  *counters = static_cast<unsigned*>(ws);
+  *scratch = static_cast<char*>(ws) + W4_WORKSPACE_COUNTER_BYTES;
+  *scratch_bytes = ws_bytes - W4_WORKSPACE_COUNTER_BYTES;
 }
 
 extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
@@ -55,24 +75,24 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
   if (((uintptr_t)x % 2) != 0 || ((uintptr_t)y % 2) != 0)
     return fail(W4_ERR_INVALID, "w4a16_gemm: x and y must be 2-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned* counters;
+  void* scratch;
+  size_t scratch_bytes;
+  split_workspace(workspace, workspace_bytes, &counters, &scratch, &scratch_bytes);
   if (M <= kDecodeM)
     return w4_gemv_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
-                          workspace, workspace_bytes, st);
+                          counters, scratch, scratch_bytes, st);
   if (M <= kSmallM)
     return w4_skinny_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y,
-                            ldy, workspace, workspace_bytes, st);
+                            ldy, scratch, scratch_bytes, st);
   return w4_prefill_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
                            st);
 }
 
-extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
-                                  void* stream) {
-  clear_error();
+static int check_grouped(const w4a16_problem* problems, int count, int64_t M) {
   if (count < 1 || count > W4_MAX_GROUPED)
     return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: count must be in [1, %d]", W4_MAX_GROUPED);
   if (!problems) return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: null problem list");
-  if (x_dtype != W4_DTYPE_BF16 && x_dtype != W4_DTYPE_FP16)
-    return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: x dtype must be bf16 or fp16");
   if (M < 1 || M > kDecodeM) return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: M must be in [1, 16]");
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
@@ -83,8 +103,32 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
       return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: bad shape in problem %d (N=%lld K=%lld G=%d)", i,
                   (long long)q.N, (long long)q.K, q.group_size);
   }
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int rc = w4_gemv_grouped_launch(problems, count, x_dtype, M, st);
-  if (rc != W4_ERR_UNSUPPORTED) return rc;
-  return w4_skinny_grouped_launch(problems, count, x_dtype, M, st);
+  return W4_OK;
+}
+
+extern "C" size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, int64_t M) {
+  clear_error();
+  if (check_grouped(problems, count, M) != W4_OK) return 0;
+  const int64_t scratch = w4_gemv_grouped_scratch_bytes(problems, count, M);
+  return scratch > 0 ? W4_WORKSPACE_COUNTER_BYTES + (size_t)scratch : 0;
+}
+
+extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  if (x_dtype != W4_DTYPE_BF16 && x_dtype != W4_DTYPE_FP16)
+    return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: x dtype must be bf16 or fp16");
+  const int rc = check_grouped(problems, count, M);
+  if (rc != W4_OK) return rc;
+  unsigned* counters;
+  void* scratch;
+  size_t scratch_bytes;
+  split_workspace(workspace, workspace_bytes, &counters, &scratch, &scratch_bytes);
+  const int lrc = w4_gemv_grouped_launch(problems, count, x_dtype, M, counters, scratch, scratch_bytes,
+                                         static_cast<hipStream_t>(stream));
+  if (lrc == W4_ERR_UNSUPPORTED && w4_last_error()[0] == '\0')
+    return fail(W4_ERR_UNSUPPORTED,
+                "w4a16_gemm_grouped: a problem exceeds 2 GiB of packed weights or the column tiles of the "
+                "split problems exceed the counter area");
+  return lrc;
 }

@@ -1,7 +1,5 @@
-// Skinny W4A16 products (1 <= M <= 64) for gfx950: the M == 1 decode GEMV,
-// the 2 <= M <= 64 split-K path with fp32 partials plus a fixed-order reduce,
-// and a grouped variant that runs several independent small-M products in one
-// launch.
+// Skinny W4A16 products (17 <= M <= 64) for gfx950: the split-K path with fp32
+// partials plus the fixed-order reduce kernel (also used by the decode path).
 //
 // Work decomposition (this library's own; the reference's Triton kernels are
 // int4_triton/gemm.py:74-157, :171-182, :185-220):
@@ -294,32 +292,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   y[m * ldy + n] = float_to_act_bits<DT>(s);
 }
 
-// Grouped launch: problem p owns tiles [tile_start[p], tile_start[p+1]).
-struct GroupedArgs {
-  SkinnyArgs prob[W4_MAX_GROUPED];
-  int64_t tile_start[W4_MAX_GROUPED + 1];
-  int vec[W4_MAX_GROUPED];
-  int count;
-};
-
-template <int DT, int MB>
-__global__ __launch_bounds__(512) void grouped_kernel(GroupedArgs g) {
-  extern __shared__ float red[];
-  const int64_t t = blockIdx.x;
-  int p = 0;
-#pragma unroll
-  for (int i = 1; i < W4_MAX_GROUPED; ++i)
-    if (i < g.count && t >= g.tile_start[i]) p = i;
-  const SkinnyArgs& a = g.prob[p];
-  const int64_t local = t - g.tile_start[p];
-  const int64_t steps_total = ((a.K >> 3) + 3) >> 2;
-  if (g.vec[p] == 4) {
-    skinny_tile<DT, 4, MB>(a, local * 64, 0, steps_total, false, 0, red);
-  } else {
-    skinny_tile<DT, 1, MB>(a, local * 16, 0, steps_total, false, 0, red);
-  }
-}
-
 }  // namespace w4
 
 // ------------------------------------------------------------------- host side
@@ -451,48 +423,4 @@ int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_
     hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_FP16>), rgrid, dim3(256), 0, st, ws, S, M, N,
                        static_cast<uint16_t*>(y), ldy);
   return check_launch("w4a16_gemm (split-K reduce)");
-}
-
-// Grouped launch with activations read from global memory (no LDS staging):
-// used when the decode kernel's staged rows would not fit in LDS.
-int w4_skinny_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M, hipStream_t st) {
-  w4::GroupedArgs g{};
-  g.count = count;
-  int64_t tiles = 0;
-  const int nw = 8;
-  for (int i = 0; i < count; ++i) {
-    const w4a16_problem& q = problems[i];
-    const int64_t G = q.group_size;
-    w4::SkinnyArgs& a = g.prob[i];
-    a.x = static_cast<const uint16_t*>(q.x);
-    a.sxm = q.K;
-    a.sxk = 1;
-    a.M = M;
-    a.qw = q.qweight;
-    a.sc = q.scales;
-    a.ze = q.zeros;
-    a.N = q.N;
-    a.K = q.K;
-    a.gshift = ilog2(G);
-    a.x_contig = ((uintptr_t)q.x % 16 == 0) && (M == 1 || q.K % 8 == 0);
-    a.sz_per_step = (G < 32 * u_for_mb(1)) ? 1 : 0;
-    a.y = q.y;
-    a.ldy = q.N;
-    a.ws = nullptr;
-    a.steps_per_split = ((q.K / 8) + 3) / 4;
-    // Balance bytes per workgroup: long-K problems get 16-column tiles so a
-    // workgroup streams about as many bytes as one 64-column tile of a short-K
-    // problem.
-    const bool vec4 = w4_skinny_vec4_ok(q.qweight, q.scales, q.zeros, q.N) && q.K <= 4096;
-    g.vec[i] = vec4 ? 4 : 1;
-    g.tile_start[i] = tiles;
-    tiles += (q.N + 16 * g.vec[i] - 1) / (16 * g.vec[i]);
-  }
-  for (int i = count; i <= W4_MAX_GROUPED; ++i) g.tile_start[i] = tiles;
-  const size_t lds = (size_t)nw * (size_t)M * 64 * sizeof(float);
-  if (x_dtype == W4_DTYPE_BF16)
-    hipLaunchKernelGGL((w4::grouped_kernel<W4_DTYPE_BF16, 1>), dim3((unsigned)tiles), dim3(nw * 64), lds, st, g);
-  else
-    hipLaunchKernelGGL((w4::grouped_kernel<W4_DTYPE_FP16, 1>), dim3((unsigned)tiles), dim3(nw * 64), lds, st, g);
-  return check_launch("w4a16_gemm_grouped");
 }

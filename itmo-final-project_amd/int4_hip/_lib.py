@@ -55,7 +55,8 @@ SIGNATURES = {
     "w4a16_workspace_bytes": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_int]),
     "w4a16_gemm": (_c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int,
                             _c_vp, _c_i64, _c_vp, _c_sz, _c_vp]),
-    "w4a16_gemm_grouped": (_c_int, [ctypes.POINTER(Problem), _c_int, _c_int, _c_i64, _c_vp]),
+    "w4a16_grouped_workspace_bytes": (_c_sz, [ctypes.POINTER(Problem), _c_int, _c_i64]),
+    "w4a16_gemm_grouped": (_c_int, [ctypes.POINTER(Problem), _c_int, _c_int, _c_i64, _c_vp, _c_sz, _c_vp]),
 }
 
 _lock = threading.Lock()

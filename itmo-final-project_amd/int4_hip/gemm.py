@@ -3,7 +3,8 @@
 Same public entry point, launch regimes and error behaviour as the reference
 (int4_triton/gemm.py:223-317):
 
-  * M == 1:        decode GEMV, one launch, no workspace;
+  * M == 1:        decode GEMV, one launch (long K split over workgroups and
+                   finished in-kernel by the last one, in split order);
   * 2 <= M <= 64:  split-K with fp32 partials and a fixed-order reduce kernel;
   * M > 64:        tiled MFMA GEMM writing the output dtype directly.
 
@@ -11,11 +12,14 @@ The kernels are hand-written HIP (itmo-final-project_amd/csrc); the split
 counts come from a static table inside the library, so results are
 bit-identical from run to run and process to process (the reference picks its
 tiles by timing, gemm.py:161-168).  Every call launches on the caller's
-current stream and never synchronizes; the split-K workspace comes from
-torch's caching allocator, so calls can be captured in a CUDA/HIP graph.
+current stream and never synchronizes.  The split-K workspace is one
+persistent zero-initialised buffer per (device, stream), allocated on the first
+call and never freed (the kernels leave its counters zero), so calls made after
+a warm-up call can be captured in a CUDA/HIP graph.
 """
 from __future__ import annotations
 
+import threading
 from typing import Sequence
 
 import torch
@@ -36,6 +40,31 @@ def _check_weight(qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tens
     return G
 
 
+_WS: dict = {}
+_WS_ALL: list = []
+_WS_LOCK = threading.Lock()
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Persistent zero-initialised split-K workspace, one per (device, stream).
+
+    The kernels leave its counter area zero, so it is reused as is; buffers are
+    never freed, so graphs that captured one keep a valid pointer.  Calls on
+    one stream are ordered, so sharing it between them is safe."""
+    key = (device.index, stream)
+    with _WS_LOCK:
+        ws = _WS.get(key)
+        if ws is not None and ws.numel() >= nbytes:
+            return ws
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("int4_hip: run this call once before graph capture "
+                               "(its split-K workspace is allocated on the first call)")
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _WS_ALL.append(ws)
+        _WS[key] = ws
+        return ws
+
+
 def w4a16_matmul(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor) -> torch.Tensor:
     """x[..., K] (bf16/fp16) @ W^T, W given as packed int4 (see quantize.py). Returns x.dtype [..., N].
 
@@ -54,16 +83,19 @@ def w4a16_matmul(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, z
     if M == 0 or N == 0:
         return y.reshape(*x.shape[:-1], N)
     lib = _lib.load()
-    ws_bytes = lib.w4a16_workspace_bytes(M, N, K, G)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
     with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        ws_bytes = lib.w4a16_workspace_bytes(M, N, K, G)
+        ws = _workspace(x.device, stream, ws_bytes) if ws_bytes else None
         rc = lib.w4a16_gemm(
             x2.data_ptr(), _XDT[x.dtype], M, N, K, x2.stride(0), x2.stride(1),
             qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(), G,
-            y.data_ptr(), N, ws.data_ptr() if ws is not None else None, ws_bytes,
-            torch.cuda.current_stream(x.device).cuda_stream)
+            y.data_ptr(), N, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+            stream)
     _lib.check(rc, "w4a16_gemm")
     return y.reshape(*x.shape[:-1], N)
+
+
 
 
 def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
@@ -98,7 +130,11 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
         outs.append(y)
     lib = _lib.load()
     with torch.cuda.device(dev):
-        rc = lib.w4a16_gemm_grouped(probs, len(xs), _XDT[dt], M, torch.cuda.current_stream(dev).cuda_stream)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        nbytes = lib.w4a16_grouped_workspace_bytes(probs, len(xs), M)
+        ws = _workspace(dev, stream, nbytes) if nbytes else None
+        rc = lib.w4a16_gemm_grouped(probs, len(xs), _XDT[dt], M, ws.data_ptr() if ws is not None else None,
+                                    ws.numel() if ws is not None else 0, stream)
     _lib.check(rc, "w4a16_gemm_grouped")
     return [y.reshape(*x.shape[:-1], y.shape[-1]) for x, y in zip(xs, outs)]
 

@@ -71,14 +71,19 @@ def test_c_abi_rejects_bad_gemm_arguments(lib):
     assert call(x=None) == _lib.ERR_INVALID
     assert call(M=0) == _lib.OK                    # empty product
     assert lib.w4a16_workspace_bytes(65, 4096, 4096, 128) == 0  # M > 64: no split-K
+    for M in (1, 8, 40):  # any workspace starts with the counter area
+        n = lib.w4a16_workspace_bytes(M, 2048, 8192, 128)
+        assert n == 0 or n > 65536
 
 
 def test_c_abi_rejects_bad_grouped_arguments(lib):
     probs = (_lib.Problem * 1)()
-    assert lib.w4a16_gemm_grouped(probs, 0, 0, 1, None) == _lib.ERR_INVALID
-    assert lib.w4a16_gemm_grouped(probs, 1, 0, 17, None) == _lib.ERR_INVALID
-    assert lib.w4a16_gemm_grouped(probs, 1, 0, 1, None) == _lib.ERR_INVALID  # null pointers
-    assert lib.w4a16_gemm_grouped(probs, _lib.MAX_GROUPED + 1, 0, 1, None) == _lib.ERR_INVALID
+    assert lib.w4a16_gemm_grouped(probs, 0, 0, 1, None, 0, None) == _lib.ERR_INVALID
+    assert lib.w4a16_gemm_grouped(probs, 1, 0, 17, None, 0, None) == _lib.ERR_INVALID
+    assert lib.w4a16_gemm_grouped(probs, 1, 0, 1, None, 0, None) == _lib.ERR_INVALID  # null pointers
+    assert lib.w4a16_gemm_grouped(probs, _lib.MAX_GROUPED + 1, 0, 1, None, 0, None) == _lib.ERR_INVALID
+    assert lib.w4a16_gemm_grouped(probs, 1, 2, 1, None, 0, None) == _lib.ERR_INVALID  # fp32 activations
+    assert lib.w4a16_grouped_workspace_bytes(probs, 0, 1) == 0
 
 
 # ---------------------------------------------------------- Python-side asserts

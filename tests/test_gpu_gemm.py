@@ -149,3 +149,30 @@ def test_graph_capture_replays_match_eager():
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
         x.mul_(1.0)
+
+
+@pytest.mark.parametrize("M", [1, 3])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_grouped_ragged_shapes(M, dtype):
+    # odd N (16-column tiles), N smaller than a tile, K long enough to split
+    shapes = [(73, 256, 32), (300, 2048, 64), (4, 8192, 128), (8, 4096, 16)]
+    ws = [_weights(N, K, G, seed=30 + i) for i, (N, K, G) in enumerate(shapes)]
+    xs = [randn((M, K), seed=40 + i, dtype=dtype).to(DEV) for i, (N, K, G) in enumerate(shapes)]
+    for _ in range(3):  # repeated calls reuse the split-K workspace (counters back at zero)
+        outs = int4_hip.w4a16_matmul_grouped(xs, ws)
+        for x, (qw, s, z), y in zip(xs, ws, outs):
+            _check(y, x, qw, s, z, ref_unrounded=False)
+
+
+def test_regimes_share_one_workspace():
+    # M=1 (in-kernel split fixup, counters) and M=16 / M=40 (split-K partials +
+    # reduce kernel) interleaved on one stream reuse the same persistent
+    # workspace; the partials must never disturb the counters.
+    qw, s, z = _weights(2048, 8192, 128, seed=21)
+    xs = {M: randn((M, 8192), seed=60 + M).to(DEV) for M in (1, 16, 40)}
+    first = {M: int4_hip.w4a16_matmul(x, qw, s, z) for M, x in xs.items()}
+    for M in (1, 16, 40):
+        _check(first[M], xs[M], qw, s, z, ref_unrounded=False)
+    for _ in range(3):
+        for M in (16, 1, 40, 1):
+            assert torch.equal(int4_hip.w4a16_matmul(xs[M], qw, s, z).view(torch.int16), first[M].view(torch.int16))
