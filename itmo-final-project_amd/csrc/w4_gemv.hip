@@ -112,10 +112,18 @@ struct Batch {
   SZ<VEC> sz[U];
 };
 
+// Byte offset that every buffer access treats as out of range (reads 0, no
+// memory traffic): used for batches past the end of a wave's run, so that the
+// load sequence of the pipelined loop is unconditional.
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
 // One workgroup: column tile at n0 (tile index tile_id), K steps [st0, st1)
 // of split `split`.  Writes y (DT) when the problem is not split, otherwise
 // fp32 partials, finished in-kernel when arrival counters are given.
-template <int DT, int VEC, int U>
+// SZS: scales/zeros loaded per step and per lane (group < 32*U, or any
+// group when batches are not U-aligned); otherwise once per batch.
+// Requires x rows dense (unit k stride, 16-byte aligned rows).
+template <int DT, int VEC, int U, bool SZS>
 __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int n0, int st0, int st1, int split, int tile_id,
                                           float* red) {
   typedef typename Act<DT>::frag F;
@@ -128,7 +136,6 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int n0, int st0, in
   const int N = a.N, K = a.K, K8 = K >> 3;
   const int M = a.M;
   const int col0 = n0 + VEC * c;
-  const bool col_full = (n0 + TN <= N);
   const uint32_t magic = fp16_magic_vgpr();
   const __amdgpu_buffer_rsrc_t rq =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, kBufferFlags);
@@ -136,43 +143,39 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int n0, int st0, in
       __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, kBufferFlags);
   const __amdgpu_buffer_rsrc_t rz =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, kBufferFlags);
+  const uint32_t x_bytes = (uint32_t)(((int64_t)(M - 1) * a.sxm + K) * 2);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)x_bytes, kBufferFlags);
   const uint32_t step_bytes = 16u * (uint32_t)N;  // four qweight rows
   const uint32_t lane_off = ((uint32_t)kb * (uint32_t)N + (uint32_t)col0) * 4u;
-  const bool gsmall = a.gshift < 5;                          // lanes of one step straddle groups
-  const uint16_t* xrow = a.x + (int64_t)(c < M ? c : M - 1) * a.sxm;
+  const uint32_t x_lane = (uint32_t)((int64_t)(c < M ? c : M - 1) * a.sxm * 2) + (uint32_t)kb * 16u;
 
-  // This wave's contiguous run of steps, a multiple of U long so that batches
-  // stay U-aligned (the launcher keeps st0 a multiple of 8).
+  // This wave's contiguous run of steps, a multiple of U long (the launcher
+  // keeps st0 a multiple of 8, so batches are U-aligned).
   const int nsteps = st1 - st0;
   const int per_wave = ((nsteps + nw - 1) / nw + U - 1) / U * U;
   const int w_begin = st0 + min(nsteps, wv * per_wave);
   const int w_end = st0 + min(nsteps, (wv + 1) * per_wave);
-  // a batch straddles groups when the group is narrower than the batch
-  const bool sz_per_step = a.gshift < 5 + __builtin_ctz(U) || (w_begin % U) != 0;
 
+  // All loads of one batch, unconditionally; a batch at or past w_end reads
+  // out-of-range offsets (zeros, no traffic).
   auto load_batch = [&](Batch<DT, VEC, U>& b, int sb) {
-    // scales/zeros first (needed first), then weights and activations per step
+    const bool live = sb < w_end;
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      if (i == 0 || sz_per_step) {
-        const int k8 = min((sb + i) * 4 + (gsmall ? kb : 0), K8 - 1);
+      if (SZS || i == 0) {
+        const int k8 = min((sb + i) * 4 + kb, K8 - 1);
         const uint32_t g = (uint32_t)((k8 * 8) >> a.gshift);
-        b.sz[i] = load_sz<VEC>(rs, rz, (g * (uint32_t)N + (uint32_t)col0) * 2u);
+        const uint32_t off = live ? (g * (uint32_t)N + (uint32_t)col0) * 2u : kOutOfRange;
+        b.sz[i] = load_sz<VEC>(rs, rz, off);
       }
     }
-    const uint32_t vo = (uint32_t)sb * step_bytes + lane_off;
-    const bool fast = col_full && (sb + U) * 4 <= K8 && sb + U <= w_end;
+    const uint32_t vo = live ? (uint32_t)sb * step_bytes + lane_off : kOutOfRange;
+    const uint32_t xo = live ? x_lane + (uint32_t)sb * 64u : kOutOfRange;
 #pragma unroll
     for (int i = 0; i < U; ++i) {
-      if (fast)
-        b.w[i] = WordT<VEC>::load(rq, vo, (uint32_t)i * step_bytes);
-      else
-        b.w[i] = WordT<VEC>::load(rq, vo + (uint32_t)i * step_bytes, 0u);
-      const int k = ((sb + i) * 4 + kb) * 8;
-      if (a.x_contig)
-        b.xa[i] = load_x8<DT, true>(xrow, k, K, 1);
-      else
-        b.xa[i] = load_x8<DT, false>(xrow, k, K, a.sxk);
+      b.w[i] = WordT<VEC>::load(rq, vo + (uint32_t)i * step_bytes, 0u);
+      b.xa[i] = __builtin_bit_cast(F, __builtin_amdgcn_raw_buffer_load_b128(rx, xo + (uint32_t)i * 64u, 0, 0));
     }
   };
 
@@ -189,47 +192,47 @@ __device__ __forceinline__ void gemv_tile(const GemvArgs& a, int n0, int st0, in
       const int step = sb + i;
       if (CHECK && step >= w_end) break;
       const int k8 = step * 4 + kb;
-      if (i == 0 || sz_per_step) {
-        // constants change at group boundaries only: keep the previous batch's
-        // when this batch continues the same group
-        const int g = (step * 32) >> a.gshift;
-        if (gsmall || g != cur_g) {
+      if (SZS) {
 #pragma unroll
-          for (int j = 0; j < VEC; ++j) gc[j] = make_group_const(b.sz[i].sj(j), b.sz[i].zj(j));
+        for (int j = 0; j < VEC; ++j) gc[j] = make_group_const(b.sz[i].sj(j), b.sz[i].zj(j));
+      } else if (i == 0) {
+        // constants change at group boundaries only: keep the previous
+        // batch's when this batch continues the same group
+        const int g = (step * 32) >> a.gshift;
+        if (g != cur_g) {
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) gc[j] = make_group_const(b.sz[0].sj(j), b.sz[0].zj(j));
           cur_g = g;
         }
       }
+      F xa = b.xa[i];
+      if (CHECK && k8 >= K8) xa = F{};  // past K: the row's next elements are not ours
 #pragma unroll
       for (int j = 0; j < VEC; ++j) {
         F bf = dequant_word<DT>(WordT<VEC>::get(b.w[i], j), gc[j], magic);
         if (CHECK && k8 >= K8) bf = F{};
-        acc[j] = Mfma<DT>::m16(b.xa[i], bf, acc[j]);
+        acc[j] = Mfma<DT>::m16(xa, bf, acc[j]);
       }
     }
   };
   auto run = [&](const Batch<DT, VEC, U>& b, int sb) {
+    if (sb >= w_end) return;
     if ((sb + U) * 4 <= K8 && sb + U <= w_end)
       compute(b, sb, std::false_type{});
     else
       compute(b, sb, std::true_type{});
   };
 
+  // Double-buffered pipeline: the loads of batch t+1 are in flight while
+  // batch t is computed.
+  Batch<DT, VEC, U> ba, bb;
   int s0 = w_begin;
-  if (s0 < w_end) {
-    Batch<DT, VEC, U> ba, bb;
-    load_batch(ba, s0);
-    while (true) {
-      int s1 = s0 + U;
-      if (s1 < w_end) load_batch(bb, s1);
-      run(ba, s0);
-      if (s1 >= w_end) break;
-      s0 = s1;
-      s1 = s0 + U;
-      if (s1 < w_end) load_batch(ba, s1);
-      run(bb, s0);
-      if (s1 >= w_end) break;
-      s0 = s1;
-    }
+  load_batch(ba, s0);
+  for (; s0 < w_end; s0 += 2 * U) {
+    load_batch(bb, s0 + U);
+    run(ba, s0);
+    load_batch(ba, s0 + 2 * U);
+    run(bb, s0 + U);
   }
 
   // ---- cross-wave reduction in wave order
@@ -299,7 +302,10 @@ __global__ __launch_bounds__(512) void gemv_kernel(GemvArgs a) {
   const int steps_total = ((a.K >> 3) + 3) >> 2;
   const int st0 = split * a.steps_per_split;
   const int st1 = min(st0 + a.steps_per_split, steps_total);
-  gemv_tile<DT, VEC, U>(a, n0, st0, st1, split, blockIdx.x, red_smem);
+  if (a.gshift < 5 + __builtin_ctz(U))
+    gemv_tile<DT, VEC, U, true>(a, n0, st0, st1, split, blockIdx.x, red_smem);
+  else
+    gemv_tile<DT, VEC, U, false>(a, n0, st0, st1, split, blockIdx.x, red_smem);
 }
 
 // Grouped launch: problem p owns workgroups [tile_start[p], tile_start[p+1]),
@@ -328,10 +334,18 @@ __global__ __launch_bounds__(512) void gemv_grouped_kernel(GemvGroupedArgs g) {
   const int steps_total = ((a.K >> 3) + 3) >> 2;
   const int st0 = split * a.steps_per_split;
   const int st1 = min(st0 + a.steps_per_split, steps_total);
-  if (g.vec[p] == 4)
-    gemv_tile<DT, 4, 2>(a, tile * 64, st0, st1, split, tile, red_smem);
-  else
-    gemv_tile<DT, 1, 2>(a, tile * 16, st0, st1, split, tile, red_smem);
+  const bool szs = a.gshift < 6;  // group < 32*U (U = 2)
+  if (g.vec[p] == 4) {
+    if (szs)
+      gemv_tile<DT, 4, 2, true>(a, tile * 64, st0, st1, split, tile, red_smem);
+    else
+      gemv_tile<DT, 4, 2, false>(a, tile * 64, st0, st1, split, tile, red_smem);
+  } else {
+    if (szs)
+      gemv_tile<DT, 1, 2, true>(a, tile * 16, st0, st1, split, tile, red_smem);
+    else
+      gemv_tile<DT, 1, 2, false>(a, tile * 16, st0, st1, split, tile, red_smem);
+  }
 }
 
 }  // namespace w4
@@ -435,7 +449,7 @@ bool plan_grouped(const w4a16_problem* problems, int count, int64_t M, GroupedPl
   size_t floats = 0, counters = 0;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
-    if (!fits_32bit(q.N, q.K)) return false;
+    if (!fits_32bit(q.N, q.K) || ((uintptr_t)q.x % 16) != 0 || M * q.K * 2 >= (1LL << 31)) return false;
     const bool vec4 = gemv_vec4_ok(q.qweight, q.scales, q.zeros, q.N);
     const int vec = vec4 ? 4 : 1;
     const int tn = 16 * vec;
@@ -492,9 +506,19 @@ int w4_gemv_grouped_launch(const w4a16_problem* problems, int count, int x_dtype
 int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_dtype, void* y, int64_t ldy,
                             hipStream_t st);
 
+int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
+                     const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, void* y, int64_t ldy,
+                     void* ws, size_t ws_bytes, hipStream_t st);
+
 int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
                    const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, void* y, int64_t ldy,
                    unsigned* counters, void* ws, size_t ws_bytes, hipStream_t st) {
+  // The decode kernel reads dense, 16-byte aligned activation rows; other
+  // layouts (strided views) take the generic skinny kernel.
+  const bool x_dense = sxk == 1 && ((uintptr_t)x % 16) == 0 && (M == 1 || (sxm % 8) == 0) &&
+                       (int64_t)M * sxm * 2 < (1LL << 31);
+  if (!x_dense)
+    return w4_skinny_launch(x, x_dtype, M, N, K, sxm, sxk, qw, sc, ze, G, y, ldy, ws, ws_bytes, st);
   if (!fits_32bit(N, K)) return fail(W4_ERR_UNSUPPORTED, "w4a16_gemm: qweight larger than 2 GiB");
   if (M == 1 && sxk == 1 && ldy == N && counters != nullptr) {
     w4a16_problem q{x, qw, sc, ze, y, N, K, G, 0};

@@ -119,6 +119,8 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
         assert x.dtype == dt and x.device == dev
         K = x.shape[-1]
         x2 = x.reshape(-1, K).contiguous()
+        if x2.data_ptr() % 16:
+            x2 = x2.clone()  # the decode kernel reads 16-byte aligned rows
         assert x2.shape[0] == M and qw.shape[0] * 8 == K
         G = _check_weight(qw, s, z, K)
         qw, s, z = qw.contiguous(), s.contiguous(), z.contiguous()
