@@ -1,0 +1,761 @@
+// Decode-shaped W4A16 products (1 <= M <= 16, group size >= 32) for gfx950:
+// one launch, no split-K, the dequantization factored out of the K loop.
+//
+// Arithmetic.  For one output column n and one quantization group g,
+//   sum_k x_k (q_k - z) s = s * ( sum_k x_k (OFF + QS q_k) - OFF xs - QS z xs ) / QS
+// with xs = sum_k x_k over the group.  The matrix core computes the first sum
+// on raw nibbles: each nibble is inserted into the mantissa of a 16-bit float
+// whose exponent is fixed, which gives OFF + QS*q exactly (bf16: 0x4300|q =
+// 128 + q; fp16: 0x6400|(q << 6) = 1024 + 64 q) with one v_and_or_b32 per two
+// nibbles.  xs comes from one more MFMA against a vector of ones.  The scale
+// and zero point are applied once per group and column in fp32 (three fused
+// multiply-adds), so the per-weight work is 7 (bf16) or 8 (fp16) VALU
+// instructions per packed word instead of a full dequantization.  W_hat is
+// never rounded to the activation dtype: the result is x @ W_hat^T with the
+// exact fp32 W_hat = (q - z) * s, accumulated in fp32 (the reference rounds
+// W_hat to the activation dtype first, int4_triton/gemm.py:139,203; both are
+// within the reference's tolerance of the exact product).
+//
+// Work decomposition.  A workgroup owns a column tile of TN = 16*VEC columns
+// over the whole K (no cross-workgroup reduction).  VEC = 4 (256-byte row
+// segments) for K <= 4096, VEC = 2 (128-byte segments, one cache line) for
+// longer K, so a workgroup streams at most 128 KB for K <= 8192.  Its eight
+// waves take contiguous runs of 32-wide K steps and stream them in chunks of
+// C steps, double buffered: the next chunk's weights, activations and
+// scales/zeros are in flight while the current one is computed.  All loads
+// are raw buffer loads; a chunk past the end of a wave's run uses an offset
+// that the hardware range check turns into zeros with no memory traffic, so
+// the load sequence is unconditional.  The per-wave partial tiles are summed
+// through LDS in wave order, so every output bit is fixed.
+//
+// Nibble order.  The four dwords built from one packed word hold nibbles
+// (0,4), (1,5), (2,6), (3,7); the activation fragment is permuted to the same
+// k order with four v_perm_b32, so the dot product is unchanged.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "w4_common.hpp"
+
+namespace w4 {
+
+struct DecArgs {
+  const uint16_t* x;
+  const uint32_t* qw;
+  const uint16_t* sc;
+  const uint16_t* ze;
+  uint16_t* y;
+  int64_t sxm;        // x row stride in elements (multiple of 8)
+  int64_t ldy;        // y row stride in elements
+  uint32_t qw_bytes;  // loads at or past these byte offsets read 0
+  uint32_t sz_bytes;
+  uint32_t x_bytes;
+  int N, K, M;
+  int gshift;  // log2(group size), >= 5
+  int vec;     // generic path: columns per lane, 4, 2 or 1
+  int cfg;     // M == 1: kCfg* tiling of dec_kernel_one
+};
+
+// M == 1 tilings (dec_kernel_one)
+constexpr int kCfgT64N8 = 0;    // 64 columns, one round of 8 loads per wave
+constexpr int kCfgT64N16 = 1;   // 64 columns, one round of 16 loads
+constexpr int kCfgT64Ring = 2;  // 64 columns, rounds of 8 loads, two in flight
+constexpr int kCfgT32N16 = 3;   // 32 columns, one round of 16 loads
+constexpr int kCfgT32Ring = 4;  // 32 columns, rounds of 8 loads, two in flight
+constexpr int kCfgVec4 = 5;     // generic path (unaligned scales or N % 8 != 0)
+constexpr int kCfgVec2 = 6;
+constexpr int kCfgVec1 = 7;
+
+struct DecGroupedArgs {
+  DecArgs prob[W4_MAX_GROUPED];
+  int wg_start[W4_MAX_GROUPED + 1];
+  int count;
+};
+
+constexpr int kDecWaves = 8;
+constexpr int kDecThreads = 64 * kDecWaves;
+constexpr uint32_t kDecOOB = 0x80000000u;  // offset the buffer range check rejects
+constexpr int kDecBufFlags = 0x00020000;   // raw buffer, 32-bit data format
+
+template <int DT>
+struct DecNum;
+template <>
+struct DecNum<W4_DTYPE_BF16> {
+  static constexpr float OFF = 128.0f, QS = 1.0f;
+  static constexpr uint32_t ONES = 0x3F803F80u;
+  static constexpr uint32_t MAGIC = 0x43004300u;
+  // nibbles (i, i+4) -> 128 + q at mantissa bits 0..3 of each half
+  __device__ __forceinline__ static u32x4 bvals(uint32_t w, uint32_t magic) {
+    u32x4 d;
+    d[0] = (w & 0x000F000Fu) | magic;
+    d[1] = ((w >> 4) & 0x000F000Fu) | magic;
+    d[2] = ((w >> 8) & 0x000F000Fu) | magic;
+    d[3] = ((w >> 12) & 0x000F000Fu) | magic;
+    return d;
+  }
+};
+template <>
+struct DecNum<W4_DTYPE_FP16> {
+  static constexpr float OFF = 1024.0f, QS = 64.0f;
+  static constexpr uint32_t ONES = 0x3C003C00u;
+  static constexpr uint32_t MAGIC = 0x64006400u;
+  // nibbles (i, i+4) -> 1024 + 64 q at mantissa bits 6..9 of each half
+  __device__ __forceinline__ static u32x4 bvals(uint32_t w, uint32_t magic) {
+    u32x4 d;
+    d[0] = ((w << 6) & 0x03C003C0u) | magic;
+    d[1] = ((w << 2) & 0x03C003C0u) | magic;
+    d[2] = ((w >> 2) & 0x03C003C0u) | magic;
+    d[3] = ((w >> 6) & 0x03C003C0u) | magic;
+    return d;
+  }
+};
+
+template <int DT>
+__device__ __forceinline__ uint32_t dec_magic_vgpr() {
+  // kept in a VGPR so each nibble pair costs one v_and_or_b32 (mask in an SGPR)
+  uint32_t m;
+  if constexpr (DT == W4_DTYPE_BF16)
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(m));
+  else
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(m));
+  return m;
+}
+
+// x[k0 .. k0+7] (dwords X0..X3 = pairs (0,1),(2,3),(4,5),(6,7)) -> the k
+// order of DecNum::bvals: pairs (0,4),(1,5),(2,6),(3,7).
+__device__ __forceinline__ u32x4 dec_perm_x(u32x4 v) {
+  u32x4 r;
+  r[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+  r[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+  r[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+  r[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+  return r;
+}
+
+template <int VEC>
+struct DecW;
+template <>
+struct DecW<4> {
+  typedef u32x4 T;
+  __device__ __forceinline__ static T load(__amdgpu_buffer_rsrc_t r, uint32_t vo) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, vo, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t get(const T& v, int j) { return v[j]; }
+};
+template <>
+struct DecW<2> {
+  typedef u32x2 T;
+  __device__ __forceinline__ static T load(__amdgpu_buffer_rsrc_t r, uint32_t vo) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, vo, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t get(const T& v, int j) { return v[j]; }
+};
+template <>
+struct DecW<1> {
+  typedef uint32_t T;
+  __device__ __forceinline__ static T load(__amdgpu_buffer_rsrc_t r, uint32_t vo) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, vo, 0, 0);
+  }
+  __device__ __forceinline__ static uint32_t get(const T& v, int) { return v; }
+};
+
+// fp16 bit patterns of the scales (or zeros) of VEC adjacent columns
+template <int VEC>
+struct DecH;
+template <>
+struct DecH<4> {
+  u32x2 v;
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  }
+  __device__ __forceinline__ float get(int j) const {
+    return half_bits_to_float((uint16_t)(v[j >> 1] >> (16 * (j & 1))));
+  }
+};
+template <>
+struct DecH<2> {
+  uint32_t v;
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  }
+  __device__ __forceinline__ float get(int j) const { return half_bits_to_float((uint16_t)(v >> (16 * j))); }
+};
+template <>
+struct DecH<1> {
+  uint32_t v;
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    v = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
+  __device__ __forceinline__ float get(int) const { return half_bits_to_float((uint16_t)v); }
+};
+
+// Generic path: steps (32-wide K slices) per chunk, two chunks in flight per
+// wave (4 KB of weights per chunk for VEC 4 and 2).
+template <int VEC>
+struct DecChunk {
+  static constexpr int C = VEC == 4 ? 4 : 8;
+  static constexpr int D = 2;
+};
+
+// One workgroup = one column tile over all of K.
+//   ONE: M == 1.  Activations travel with each chunk (lanes 0..4C-1 load one
+//        8-element k slice each), are permuted once and shared through LDS;
+//        all 16 rows of the MFMA operand repeat row 0, so only element 0 of
+//        each accumulator is corrected and reduced.
+//   !ONE: rows 0..M-1 (lanes with c >= M repeat row M-1); each lane loads and
+//        permutes its own fragment every step.
+// GS = correction interval in steps (min(group size / 32, C)).
+template <int DT, int VEC, bool ONE, int GS>
+__device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red, uint32_t* xl) {
+  typedef typename Act<DT>::frag F;
+  typedef DecNum<DT> Num;
+  typedef typename DecW<VEC>::T WT;
+  constexpr int TN = 16 * VEC;
+  constexpr int C = DecChunk<VEC>::C;
+  constexpr int D = DecChunk<VEC>::D;
+  constexpr int NP = C / GS;  // correction points per chunk
+  constexpr int R = ONE ? 1 : 4;
+  static_assert(GS >= 1 && GS <= C && (C % GS) == 0, "correction interval");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: run bounds stay scalar
+  const int c = lane & 15, kb = lane >> 4;
+  const int N = a.N, K = a.K, M = a.M;
+  const int n0 = tile * TN;
+  const int S = K >> 5;
+  const int per_wave = ((S + kDecWaves - 1) / kDecWaves + C - 1) / C * C;
+  const int wb = min(S, wv * per_wave);
+  const int we = min(S, wb + per_wave);
+
+  const __amdgpu_buffer_rsrc_t rq =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, kDecBufFlags);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, kDecBufFlags);
+  const __amdgpu_buffer_rsrc_t rz =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, kDecBufFlags);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kDecBufFlags);
+
+  const uint32_t step_bytes = 16u * (uint32_t)N;  // four qweight rows
+  const uint32_t col = (uint32_t)(n0 + VEC * c);
+  const uint32_t w_lane = ((uint32_t)kb * (uint32_t)N + col) * 4u;
+  const uint32_t sz_lane = col * 2u;
+  // ONE: lane l < 4C carries k8 row 4*sb + l of the chunk; !ONE: own row, own kb
+  const uint32_t x_lane = ONE ? (uint32_t)lane * 16u
+                              : (uint32_t)((int64_t)min(c, M - 1) * a.sxm * 2) + (uint32_t)kb * 16u;
+  const uint32_t magic = dec_magic_vgpr<DT>();
+  const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
+
+  struct Chunk {
+    WT w[C];
+    DecH<VEC> s[NP], z[NP];
+    u32x4 xv[ONE ? 1 : C];
+  };
+
+  // Out-of-range offsets are formed by OR-ing bit 31 in (never by selecting
+  // between two offsets), so the compiler keeps every load unconditional.
+  // Scheduling barriers pin the issue order (activations, scales/zeros,
+  // weights; chunk after chunk) to the order of use, so the waits at the loop
+  // head count only the older chunk's loads.
+  const uint32_t x_lane_oob = (ONE && lane >= 4 * C) ? kDecOOB : 0u;
+  auto load_chunk = [&](Chunk& ch, int sb) {
+    const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (ONE) {
+      const uint32_t xo = ((uint32_t)sb * 64u + x_lane) | x_lane_oob | oob;
+      ch.xv[0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const uint32_t g = (uint32_t)(((sb + p * GS) * 32) >> a.gshift);
+      const uint32_t off = (g * (uint32_t)N * 2u + sz_lane) | oob;
+      ch.s[p].load(rs, off);
+      ch.z[p].load(rz, off);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t vo = ((uint32_t)sb * step_bytes + w_lane) | oob;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+      ch.w[i] = DecW<VEC>::load(rq, vo + (uint32_t)i * step_bytes);
+      if constexpr (!ONE) {
+        // steps past K read 0 (rows of other activations must not leak in)
+        const uint32_t xoob = sb + i < S ? oob : kDecOOB;
+        ch.xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ((uint32_t)(sb + i) * 64u + x_lane) | xoob, 0, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  f32x4 acc[VEC];
+  f32x4 xs;
+  float tot[VEC][R];
+#pragma unroll
+  for (int j = 0; j < VEC; ++j)
+#pragma unroll
+    for (int r = 0; r < R; ++r) tot[j][r] = 0.0f;
+
+  auto compute_chunk = [&](const Chunk& ch) {
+    if constexpr (ONE) {
+      // share this chunk's activations: slot l holds k8 row 4*sb + l, permuted
+      const u32x4 v = dec_perm_x(ch.xv[0]);
+      *reinterpret_cast<u32x4*>(xl + (wv * 64 + lane) * 4) = v;
+      __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+#pragma unroll
+      for (int i = 0; i < GS; ++i) {
+        const int st = p * GS + i;
+        F xa;
+        if constexpr (ONE)
+          xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(xl + (wv * 64 + st * 4 + kb) * 4));
+        else
+          xa = __builtin_bit_cast(F, dec_perm_x(ch.xv[st]));
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const F b = __builtin_bit_cast(F, Num::bvals(DecW<VEC>::get(ch.w[st], j), magic));
+          acc[j] = Mfma<DT>::m16(xa, b, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[j]);
+        }
+        xs = Mfma<DT>::m16(xa, ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs);
+      }
+      // QS * sum x (q - z) = acc - OFF xs - z (QS xs); tot accumulates s times it
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float ox = Num::OFF * xs[r];
+        const float qx = Num::QS * xs[r];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          const float u = __builtin_fmaf(-ch.z[p].get(j), qx, acc[j][r] - ox);
+          tot[j][r] = __builtin_fmaf(ch.s[p].get(j), u, tot[j][r]);
+        }
+      }
+    }
+    if constexpr (ONE) __builtin_amdgcn_wave_barrier();  // slots are rewritten by the next chunk
+  };
+
+  // Ring of D chunks: chunk t + D is loaded as soon as chunk t is consumed.
+  // Loads are unconditional (a chunk past the run reads out of range: zeros,
+  // no traffic), so the compiler's waits stay exact; computing a chunk past
+  // the run is skipped with a scalar branch that contains no load.
+  Chunk ring[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) load_chunk(ring[d], wb + d * C);
+  for (int sb = wb; sb < we; sb += D * C) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      if (d == 0 || sb + d * C < we) compute_chunk(ring[d]);
+      load_chunk(ring[d], sb + (d + D) * C);
+    }
+  }
+
+  // cross-wave reduction in wave order
+  if (ONE ? kb == 0 : true) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int m = ONE ? 0 : kb * 4 + r;
+      if (m < M) {
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) red[(wv * M + m) * TN + VEC * c + j] = tot[j][r];
+      }
+    }
+  }
+  __syncthreads();
+  const int total = M * TN;
+  for (int idx = tid; idx < total; idx += kDecThreads) {
+    const int m = idx / TN;
+    const int nl = idx - m * TN;
+    const int n = n0 + nl;
+    if (n >= N) continue;
+    float s = red[m * TN + nl];
+#pragma unroll
+    for (int w = 1; w < kDecWaves; ++w) s += red[(w * M + m) * TN + nl];
+    a.y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(s * (1.0f / Num::QS));
+  }
+}
+
+// ---------------------------------------------------------------- M == 1 path
+//
+// Every wave issues all loads of a round (NL 128-bit weight loads per lane,
+// plus one or two loads each for the round's activations, scales and zeros)
+// before it waits for any of them; with NL = 8 or 16 a round is a wave's
+// whole run for the common shapes, so a workgroup exposes one memory latency.
+//
+// Column tiles (always four columns per lane, 128-bit weight loads):
+//   T64: 64 columns; lane l = (quad c = l % 16, row kb = l / 16): a load step
+//        covers 4 qweight rows (32 k) x 256 bytes.
+//   T32: 32 columns; lane l = (quad c = l % 8, row r = l / 8): a load step
+//        covers 8 qweight rows (64 k) x 128 bytes (one cache line a row).  In
+//        the 16x16x32 MFMA, lanes l and l + 8 share a k slice but carry
+//        different rows, so row 0 / column n < 8 of the result sums the even
+//        rows and row 8 / column n + 8 the odd rows of quad n; each half is
+//        corrected with its own activation sum and the halves are added in
+//        the final reduction.
+// Activations (permuted to the nibble order), scales and zeros are staged in
+// a per-wave LDS area that only the wave itself reads (no barrier).
+constexpr int kOneWaveLds = 6144;  // per wave: activations 2 KB, scales 2 KB, zeros 2 KB
+constexpr int kOneRedOffset = kDecWaves * kOneWaveLds;
+
+template <int DT, int TILE, int GSI, int NL, int D>
+__device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t* lds) {
+  typedef typename Act<DT>::frag F;
+  typedef DecNum<DT> Num;
+  constexpr bool T32 = TILE == 32;
+  constexpr int SK = T32 ? 64 : 32;          // k per load step
+  constexpr int RPS = SK / 8;                // qweight rows per load step
+  constexpr int GS = GSI < NL ? GSI : NL;    // correction interval (steps)
+  constexpr int NP = NL / GS;                // correction points = staged groups per round
+  constexpr int LPG = TILE * 2 / 16;         // lanes per staged group row (16 B each)
+  constexpr int SZL = (NP * LPG + 63) / 64;  // scale (and zero) loads per round
+  constexpr int XE = NL * RPS;               // activation entries (8 k) per round
+  constexpr int XL = (XE + 63) / 64;         // activation loads per round
+  static_assert(XE * 16 <= 2048 && SZL * 1024 <= 2048, "per-wave LDS area");
+  static_assert(GSI >= 1 && (NL % GS) == 0, "correction interval");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cq = T32 ? (lane & 7) : (lane & 15);
+  const int rr = T32 ? (lane >> 3) : (lane >> 4);
+  const int N = a.N, K = a.K;
+  const int n0 = tile * TILE;
+  const int S = K / SK;
+  const int per_wave = ((S + kDecWaves - 1) / kDecWaves + NL - 1) / NL * NL;
+  const int wb = min(S, wv * per_wave);
+  const int we = min(S, wb + per_wave);
+
+  const __amdgpu_buffer_rsrc_t rq =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, kDecBufFlags);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, kDecBufFlags);
+  const __amdgpu_buffer_rsrc_t rz =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, kDecBufFlags);
+  const __amdgpu_buffer_rsrc_t rx =
+      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kDecBufFlags);
+
+  const uint32_t step_bytes = (uint32_t)RPS * 4u * (uint32_t)N;
+  const uint32_t w_lane = ((uint32_t)rr * (uint32_t)N + (uint32_t)(n0 + 4 * cq)) * 4u;
+  const uint32_t sz_row = (uint32_t)(lane / LPG);
+  const uint32_t sz_col = (uint32_t)(n0 * 2 + (lane % LPG) * 16);
+  uint8_t* x_lds = lds + wv * kOneWaveLds;
+  uint8_t* s_lds = x_lds + 2048;
+  uint8_t* z_lds = x_lds + 4096;
+  const uint32_t magic = dec_magic_vgpr<DT>();
+  const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
+
+  struct Round {
+    u32x4 w[NL];
+    u32x4 x[XL];
+    u32x4 s[SZL], z[SZL];
+  };
+  // Issue order = order of use: activations, scales, zeros, weights.
+  auto load_round = [&](Round& r, int sb) {
+    const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < XL; ++i) {
+      const uint32_t e = (uint32_t)(lane + 64 * i);
+      const uint32_t eoob = e < (uint32_t)XE ? 0u : kDecOOB;
+      r.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (((uint32_t)sb * RPS + e) * 16u) | eoob | oob, 0, 0);
+    }
+    const uint32_t g0 = (uint32_t)((sb * SK) >> a.gshift);
+#pragma unroll
+    for (int i = 0; i < SZL; ++i) {
+      const uint32_t gr = sz_row + (uint32_t)(64 / LPG) * i;
+      const uint32_t goob = gr < (uint32_t)NP ? 0u : kDecOOB;
+      const uint32_t off = ((g0 + gr) * (uint32_t)N * 2u + sz_col) | goob | oob;
+      r.s[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+      r.z[i] = __builtin_amdgcn_raw_buffer_load_b128(rz, off, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t vo = ((uint32_t)sb * step_bytes + w_lane) | oob;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, vo + (uint32_t)i * step_bytes, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  f32x4 acc[4];
+  f32x4 xs;
+  float tot[4] = {0.f, 0.f, 0.f, 0.f};
+
+  auto compute_round = [&](const Round& r) {
+    // stage this round's activations (permuted), scales and zeros
+#pragma unroll
+    for (int i = 0; i < XL; ++i)
+      *reinterpret_cast<u32x4*>(x_lds + (lane + 64 * i) * 16) = dec_perm_x(r.x[i]);
+#pragma unroll
+    for (int i = 0; i < SZL; ++i) {
+      *reinterpret_cast<u32x4*>(s_lds + (lane + 64 * i) * 16) = r.s[i];
+      *reinterpret_cast<u32x4*>(z_lds + (lane + 64 * i) * 16) = r.z[i];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+#pragma unroll
+      for (int i = 0; i < GS; ++i) {
+        const int st = p * GS + i;
+        const F xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(x_lds + (st * RPS + rr) * 16));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const F b = __builtin_bit_cast(F, Num::bvals(r.w[st][j], magic));
+          acc[j] = Mfma<DT>::m16(xa, b, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[j]);
+        }
+        xs = Mfma<DT>::m16(xa, ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs);
+      }
+      const int gp = (p * GS * SK) >> a.gshift;  // staged group row of this point
+      const u32x2 sv = *reinterpret_cast<const u32x2*>(s_lds + gp * TILE * 2 + cq * 8);
+      const u32x2 zv = *reinterpret_cast<const u32x2*>(z_lds + gp * TILE * 2 + cq * 8);
+      const float ox = Num::OFF * xs[0];
+      const float qx = Num::QS * xs[0];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float sj = half_bits_to_float((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
+        const float zj = half_bits_to_float((uint16_t)(zv[j >> 1] >> (16 * (j & 1))));
+        const float u = __builtin_fmaf(-zj, qx, acc[j][0] - ox);
+        tot[j] = __builtin_fmaf(sj, u, tot[j]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the next round rewrites the staging area
+  };
+
+  if constexpr (D == 1) {
+    // the host picks D == 1 only when a wave's run fits in one round
+    if (wb < we) {
+      Round r;
+      load_round(r, wb);
+      compute_round(r);
+    }
+  } else {
+    Round ra, rb;
+    load_round(ra, wb);
+    load_round(rb, wb + NL);
+    for (int sb = wb; sb < we; sb += 2 * NL) {
+      compute_round(ra);
+      load_round(ra, sb + 2 * NL);
+      if (sb + NL < we) compute_round(rb);
+      load_round(rb, sb + 3 * NL);
+    }
+  }
+
+  // cross-wave (and, T32, even/odd half) reduction in a fixed order
+  float* red = reinterpret_cast<float*>(lds + kOneRedOffset);
+  // T64: row 0 = lanes 0..15.  T32: row 0 / columns 0..7 = lanes 0..7 (even
+  // rows), row 8 / columns 8..15 = lanes 40..47 (odd rows).
+  const bool owner = T32 ? (lane < 8 || (lane >= 40 && lane < 48)) : lane < 16;
+  if (owner) {
+    const int half = T32 && lane >= 40 ? 1 : 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) red[wv * 64 + half * 32 + 4 * cq + j] = tot[j];
+  }
+  __syncthreads();
+  if (tid < TILE) {
+    const int n = n0 + tid;
+    if (n < N) {
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kDecWaves; ++w) {
+        v += red[w * 64 + tid];
+        if constexpr (T32) v += red[w * 64 + 32 + tid];
+      }
+      a.y[n] = float_to_act_bits<DT>(v * (1.0f / Num::QS));
+    }
+  }
+}
+
+template <int DT, int GC>
+__global__ __launch_bounds__(kDecThreads) void dec_kernel_one(DecGroupedArgs g) {
+  extern __shared__ __attribute__((aligned(16))) float dec_smem[];
+  const int t = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < W4_MAX_GROUPED; ++i)
+    if (i < g.count && t >= g.wg_start[i]) p = i;
+  const DecArgs& a = g.prob[p];
+  const int tile = t - g.wg_start[p];
+  uint8_t* lds = reinterpret_cast<uint8_t*>(dec_smem);
+  constexpr int G64 = 1 << GC;                 // steps per group, 32-k steps
+  constexpr int G32 = GC >= 1 ? (1 << (GC - 1)) : 1;  // 64-k steps (T32 needs group >= 64)
+  constexpr int GSO = G64 < 8 ? G64 : 8;       // generic-path interval
+  switch (a.cfg) {
+    case kCfgT64N8: dec_tile_one<DT, 64, G64, 8, 1>(a, tile, lds); break;
+    case kCfgT64N16: dec_tile_one<DT, 64, G64, 16, 1>(a, tile, lds); break;
+    case kCfgT64Ring: dec_tile_one<DT, 64, G64, 8, 2>(a, tile, lds); break;
+    case kCfgT32N16: dec_tile_one<DT, 32, G32, 16, 1>(a, tile, lds); break;
+    case kCfgT32Ring: dec_tile_one<DT, 32, G32, 8, 2>(a, tile, lds); break;
+    case kCfgVec4: dec_tile<DT, 4, true, (GSO < 4 ? GSO : 4)>(a, tile, dec_smem + kDecWaves * 64 * 4, reinterpret_cast<uint32_t*>(dec_smem)); break;
+    case kCfgVec2: dec_tile<DT, 2, true, GSO>(a, tile, dec_smem + kDecWaves * 64 * 4, reinterpret_cast<uint32_t*>(dec_smem)); break;
+    default: dec_tile<DT, 1, true, GSO>(a, tile, dec_smem + kDecWaves * 64 * 4, reinterpret_cast<uint32_t*>(dec_smem)); break;
+  }
+}
+
+template <int DT, bool ONE, int GS>
+__global__ __launch_bounds__(kDecThreads) void dec_kernel(DecGroupedArgs g) {
+  extern __shared__ __attribute__((aligned(16))) float dec_smem[];
+  const int t = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < W4_MAX_GROUPED; ++i)
+    if (i < g.count && t >= g.wg_start[i]) p = i;
+  const DecArgs& a = g.prob[p];
+  const int tile = t - g.wg_start[p];
+  // LDS: [activation slots, ONE only: 8 waves x 64 x 16 B][reduction]
+  uint32_t* xl = reinterpret_cast<uint32_t*>(dec_smem);
+  float* red = dec_smem + (ONE ? kDecWaves * 64 * 4 : 0);
+  if (a.vec == 4)
+    dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4)>(a, tile, red, xl);
+  else if (a.vec == 2)
+    dec_tile<DT, 2, ONE, GS>(a, tile, red, xl);
+  else
+    dec_tile<DT, 1, ONE, GS>(a, tile, red, xl);
+}
+
+}  // namespace w4
+
+// ------------------------------------------------------------------- host side
+using namespace w4host;
+
+namespace {
+
+bool dec_fits_32bit(int64_t N, int64_t K) {
+  return N > 0 && K > 0 && N < (1LL << 27) && K < (1LL << 30) && (K / 8) * N * 4 < (1LL << 31);
+}
+
+struct DecPlan {
+  w4::DecGroupedArgs g;
+  int wgs;
+  int gs;  // correction interval class (1, 2, 4, 8)
+  size_t lds;
+};
+
+// Launch table: a pure function of shapes, strides and pointer alignment.
+// Returns false (nothing launched) when a problem needs the general kernels:
+// group size < 32, mixed group-size classes, misaligned or non-dense
+// activations, or offsets past 2 GiB.
+bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int64_t M,
+              DecPlan& dp) {
+  dp = DecPlan{};
+  if (count < 1 || count > W4_MAX_GROUPED || M < 1 || M > 16) return false;
+  struct Item {
+    int idx;
+    int vec, cfg, tile_n;
+    int64_t tiles, bytes_per_wg;
+  } items[W4_MAX_GROUPED];
+  int gclass = -1;
+  bool one_path = false;
+  for (int i = 0; i < count; ++i) {
+    const w4a16_problem& q = problems[i];
+    if (!dec_fits_32bit(q.N, q.K) || q.group_size < 32 || !is_pow2(q.group_size)) return false;
+    // M == 1: log2(G / 32) capped at 4; M > 1: min(G / 32, 8).  One class per launch.
+    const int cls = M == 1 ? std::min(ilog2(q.group_size) - 5, 4) : (int)std::min<int64_t>(q.group_size / 32, 8);
+    if (gclass >= 0 && cls != gclass) return false;
+    gclass = cls;
+    if (((uintptr_t)q.x % 16) != 0) return false;
+    if (M > 1 && ((sxm[i] % 8) != 0 || sxm[i] < q.K || ((M - 1) * sxm[i] + q.K) * 2 >= (1LL << 31))) return false;
+    if (ldy != nullptr && ldy[i] < q.N) return false;
+    const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
+    int vec = 1, cfg = w4::kCfgVec1, tn = 16;
+    if (M == 1 && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0) {
+      // one-round M == 1 tilings: 64 columns up to K = 4096, 32 columns beyond
+      const bool t32 = q.K > 4096 && q.group_size >= 64;
+      const int64_t steps = q.K / (t32 ? 64 : 32);
+      const int64_t per_wave = (steps + w4::kDecWaves - 1) / w4::kDecWaves;
+      tn = t32 ? 32 : 64;
+      vec = 4;
+      if (t32)
+        cfg = per_wave <= 16 ? w4::kCfgT32N16 : w4::kCfgT32Ring;
+      else
+        cfg = per_wave <= 8 ? w4::kCfgT64N8 : per_wave <= 16 ? w4::kCfgT64N16 : w4::kCfgT64Ring;
+      one_path = true;
+    } else if (q.N % 4 == 0 && qa % 16 == 0 && sa % 8 == 0 && za % 8 == 0 && q.K <= 4096) {
+      vec = 4, cfg = w4::kCfgVec4, tn = 64;
+    } else if (q.N % 2 == 0 && qa % 8 == 0 && sa % 4 == 0 && za % 4 == 0) {
+      vec = 2, cfg = w4::kCfgVec2, tn = 32;
+    }
+    items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn, (int64_t)tn * q.K / 2};
+  }
+  // largest workgroups first, so the longest-running ones start first
+  std::stable_sort(items, items + count, [](const Item& l, const Item& r) { return l.bytes_per_wg > r.bytes_per_wg; });
+  int wgs = 0;
+  for (int s = 0; s < count; ++s) {
+    const Item& it = items[s];
+    const w4a16_problem& q = problems[it.idx];
+    w4::DecArgs& a = dp.g.prob[s];
+    a.x = static_cast<const uint16_t*>(q.x);
+    a.qw = reinterpret_cast<const uint32_t*>(q.qweight);
+    a.sc = q.scales;
+    a.ze = q.zeros;
+    a.y = static_cast<uint16_t*>(q.y);
+    a.sxm = M > 1 ? sxm[it.idx] : 0;
+    a.ldy = ldy != nullptr ? ldy[it.idx] : q.N;
+    a.qw_bytes = (uint32_t)((q.K / 8) * q.N * 4);
+    a.sz_bytes = (uint32_t)((q.K / q.group_size) * q.N * 2);
+    a.x_bytes = (uint32_t)(((M - 1) * a.sxm + q.K) * 2);
+    a.N = (int)q.N;
+    a.K = (int)q.K;
+    a.M = (int)M;
+    a.gshift = ilog2(q.group_size);
+    a.vec = it.vec;
+    a.cfg = it.cfg;
+    dp.g.wg_start[s] = wgs;
+    if (it.tiles > (1 << 24)) return false;
+    wgs += (int)it.tiles;
+  }
+  for (int s = count; s <= W4_MAX_GROUPED; ++s) dp.g.wg_start[s] = wgs;
+  dp.g.count = count;
+  dp.wgs = wgs;
+  dp.gs = gclass;
+  if (M == 1)  // per-wave staging areas (or the generic activation slots) + reduction
+    dp.lds = (one_path ? (size_t)w4::kOneRedOffset : (size_t)w4::kDecWaves * 64 * 16) +
+             (size_t)w4::kDecWaves * 64 * sizeof(float);
+  else
+    dp.lds = (size_t)w4::kDecWaves * M * 64 * sizeof(float);
+  return wgs > 0;
+}
+
+template <int DT>
+void dec_launch_one(const DecPlan& dp, hipStream_t st) {
+  const dim3 grid((unsigned)dp.wgs), block(w4::kDecThreads);
+  switch (dp.gs) {
+    case 0: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 0>), grid, block, dp.lds, st, dp.g); break;
+    case 1: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 1>), grid, block, dp.lds, st, dp.g); break;
+    case 2: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 2>), grid, block, dp.lds, st, dp.g); break;
+    case 3: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 3>), grid, block, dp.lds, st, dp.g); break;
+    default: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 4>), grid, block, dp.lds, st, dp.g); break;
+  }
+}
+
+template <int DT>
+void dec_launch_rows(const DecPlan& dp, hipStream_t st) {
+  const dim3 grid((unsigned)dp.wgs), block(w4::kDecThreads);
+  switch (dp.gs) {
+    case 1: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 1>), grid, block, dp.lds, st, dp.g); break;
+    case 2: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 2>), grid, block, dp.lds, st, dp.g); break;
+    case 4: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 4>), grid, block, dp.lds, st, dp.g); break;
+    default: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 8>), grid, block, dp.lds, st, dp.g); break;
+  }
+}
+
+}  // namespace
+
+// Factored decode launch (see the top of this file).  Returns
+// W4_ERR_UNSUPPORTED, with nothing launched and no error message, when the
+// problems need the general kernels.  sxm: activation row strides, ldy: output
+// row strides (elements; null = dense).
+int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
+                     int x_dtype, int64_t M, hipStream_t st) {
+  DecPlan dp;
+  if (!dec_plan(problems, sxm, ldy, count, M, dp)) return W4_ERR_UNSUPPORTED;
+  if (x_dtype == W4_DTYPE_BF16) {
+    if (M == 1)
+      dec_launch_one<W4_DTYPE_BF16>(dp, st);
+    else
+      dec_launch_rows<W4_DTYPE_BF16>(dp, st);
+  } else {
+    if (M == 1)
+      dec_launch_one<W4_DTYPE_FP16>(dp, st);
+    else
+      dec_launch_rows<W4_DTYPE_FP16>(dp, st);
+  }
+  return check_launch("w4a16 decode");
+}

@@ -510,6 +510,9 @@ int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K
                      const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, void* y, int64_t ldy,
                      void* ws, size_t ws_bytes, hipStream_t st);
 
+int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
+                     int x_dtype, int64_t M, hipStream_t st);
+
 int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
                    const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, void* y, int64_t ldy,
                    unsigned* counters, void* ws, size_t ws_bytes, hipStream_t st) {
@@ -520,6 +523,12 @@ int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, 
   if (!x_dense)
     return w4_skinny_launch(x, x_dtype, M, N, K, sxm, sxk, qw, sc, ze, G, y, ldy, ws, ws_bytes, st);
   if (!fits_32bit(N, K)) return fail(W4_ERR_UNSUPPORTED, "w4a16_gemm: qweight larger than 2 GiB");
+  {
+    // group size >= 32: factored single-launch decode kernel (w4_decode.hip)
+    const w4a16_problem q{x, qw, sc, ze, y, N, K, G, 0};
+    const int rc = w4_decode_launch(&q, &sxm, &ldy, 1, x_dtype, M, st);
+    if (rc != W4_ERR_UNSUPPORTED) return rc;
+  }
   if (M == 1 && sxk == 1 && ldy == N && counters != nullptr) {
     w4a16_problem q{x, qw, sc, ze, y, N, K, G, 0};
     const int rc = w4_gemv_grouped_launch(&q, 1, x_dtype, 1, counters, ws, ws_bytes, st);
@@ -559,6 +568,12 @@ int64_t w4_gemv_grouped_scratch_bytes(const w4a16_problem* problems, int count, 
 // exceed the counter area.
 int w4_gemv_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
                            unsigned* counters, void* scratch, size_t scratch_bytes, hipStream_t st) {
+  if (count >= 1 && count <= W4_MAX_GROUPED) {
+    int64_t sxm[W4_MAX_GROUPED];
+    for (int i = 0; i < count; ++i) sxm[i] = problems[i].K;
+    const int rc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, M, st);
+    if (rc != W4_ERR_UNSUPPORTED) return rc;
+  }
   GroupedPlan gp;
   if (!plan_grouped(problems, count, M, gp)) return W4_ERR_UNSUPPORTED;
   if (gp.counter_bytes > 0) {

@@ -9,6 +9,16 @@ Tolerances (stated per the task's floating-point bar):
   accumulation error;
 * the reference's own check against the unrounded fp32 W_hat
   (tests/test_kernels.py:60): rtol 2e-2, atol 2e-2 * max |ref|.
+
+The decode regime (M <= 16, group size >= 32, dense activation rows) applies
+scales and zero points after the matrix-core sums, so it multiplies by the
+exact fp32 W_hat instead of W_hat rounded to the activation dtype.  Its
+elementwise check is against ref = x @ W_hat_fp32^T with
+``|y - ref| <= u_out * |ref| + c * sum_k |x_k| s_{g(k)}``: the fp32 rounding of
+the per-group sums of x_k * (OFF + QS q_k), whose terms are at most 143 |x_k|
+(bf16: 128 + q) or 31 |x_k| (fp16: (1024 + 64 q) / 64), c = 2**-10 (bf16),
+2**-12 (fp16).  A wrong zero point, scale, nibble or group is off by about
+s * |sum_g x|, orders of magnitude above that slack.
 """
 import numpy as np
 import pytest
@@ -23,19 +33,31 @@ DEV = "cuda"
 U_OUT = {torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
 
 
-def _check(out: torch.Tensor, x: torch.Tensor, qw, s, z, ref_unrounded: bool = True):
+def _decode(M: int, G: int) -> bool:
+    """True when w4a16_matmul takes the factored decode kernel (dense rows)."""
+    return M <= 16 and G >= 32
+
+
+def _check(out: torch.Tensor, x: torch.Tensor, qw, s, z, ref_unrounded: bool = True, exact_w: bool = False):
     xd = dtype_name(x.dtype)
     x2 = x.reshape(-1, x.shape[-1])
     qn, sn, zn = qw.cpu().numpy(), bits_of(s), bits_of(z)
-    ref = O.w4a16_matmul(bits_of(x2), xd, qn, sn, zn)               # float64
-    w_hat = O.dequantize_int4(qn, sn, zn, xd).astype(np.float64)
-    mag = np.abs(O.half_bits_to_f32(bits_of(x2), xd).astype(np.float64)) @ np.abs(w_hat).T
+    xa = np.abs(O.half_bits_to_f32(bits_of(x2), xd).astype(np.float64))
+    if exact_w:
+        ref = O.w4a16_matmul(bits_of(x2), xd, qn, sn, zn, w_hat_dtype="fp32")  # float64
+        G = x2.shape[1] // sn.shape[0]
+        s_abs = np.abs(O.half_bits_to_f32(sn, "fp16").astype(np.float64))
+        slack = (2.0**-10 if x.dtype == torch.bfloat16 else 2.0**-12) * (xa @ np.repeat(s_abs, G, axis=0))
+    else:
+        ref = O.w4a16_matmul(bits_of(x2), xd, qn, sn, zn)               # float64
+        w_hat = O.dequantize_int4(qn, sn, zn, xd).astype(np.float64)
+        slack = 2.0**-20 * (xa @ np.abs(w_hat).T)
     y = out.reshape(-1, out.shape[-1]).float().cpu().numpy().astype(np.float64)
     assert y.shape == ref.shape
     err = np.abs(y - ref)
     scale = max(np.abs(ref).max(), 1e-30)
     assert err.max() <= 1e-2 * scale, f"max rel err {err.max() / scale:.3e}"
-    bound = U_OUT[x.dtype] * np.abs(ref) + 2.0**-20 * mag + 1e-30
+    bound = U_OUT[x.dtype] * np.abs(ref) + slack + 1e-30
     bad = err > bound
     assert not bad.any(), f"{int(bad.sum())} elements outside the elementwise bound, first {np.argwhere(bad)[0]}"
     if ref_unrounded:
@@ -60,7 +82,7 @@ def test_w4a16_matmul(M, NK, dtype):
     x = randn((M, K), seed=M, dtype=dtype).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
     assert out.dtype == dtype and out.shape == (M, N)
-    _check(out, x, qw, s, z)
+    _check(out, x, qw, s, z, exact_w=_decode(M, 128))
 
 
 # split-K regime over the block's shapes and the three group sizes
@@ -73,7 +95,7 @@ def test_split_k_regime(M, NK, G):
     qw, s, z = _weights(N, K, G, seed=7 * N + K + G)
     x = randn((M, K), seed=100 + M).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
-    _check(out, x, qw, s, z, ref_unrounded=False)
+    _check(out, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, G))
     # bit-identical repeat runs, with the workspace poisoned in between
     junk = torch.full((64 << 20,), float("nan"), device=DEV)
     del junk
@@ -126,7 +148,10 @@ def test_grouped_matches_single(M):
     xs = [randn((M, K), seed=50 + i).to(DEV) for i, (N, K) in enumerate(shapes)]
     outs = int4_hip.w4a16_matmul_grouped(xs, ws)
     for x, (qw, s, z), y in zip(xs, ws, outs):
-        _check(y, x, qw, s, z, ref_unrounded=False)
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+    singles = [int4_hip.w4a16_matmul(x, *w) for x, w in zip(xs, ws)]
+    for a, b in zip(outs, singles):  # one problem per launch: same tiles, same bits
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     again = int4_hip.w4a16_matmul_grouped(xs, ws)
     for a, b in zip(outs, again):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
@@ -172,7 +197,23 @@ def test_regimes_share_one_workspace():
     xs = {M: randn((M, 8192), seed=60 + M).to(DEV) for M in (1, 16, 40)}
     first = {M: int4_hip.w4a16_matmul(x, qw, s, z) for M, x in xs.items()}
     for M in (1, 16, 40):
-        _check(first[M], xs[M], qw, s, z, ref_unrounded=False)
+        _check(first[M], xs[M], qw, s, z, ref_unrounded=False, exact_w=_decode(M, 128))
     for _ in range(3):
         for M in (16, 1, 40, 1):
             assert torch.equal(int4_hip.w4a16_matmul(xs[M], qw, s, z).view(torch.int16), first[M].view(torch.int16))
+
+
+# factored decode kernel: odd N (one column per lane), N below one tile, long K
+# (32-column tiles), K with a tail chunk, group sizes of every correction class
+@pytest.mark.parametrize("G", [32, 128, 256])
+@pytest.mark.parametrize("M", [1, 3, 16])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_ragged_shapes(M, dtype, G):
+    shapes = [(N, K) for N, K in [(73, 256), (300, 2048), (4, 8192), (8, 4352), (24, 1024 + G)] if K % G == 0]
+    print(f"[decode] M={M} G={G} {dtype} shapes={shapes}", flush=True)
+    ws = [_weights(N, K, G, seed=70 + i) for i, (N, K) in enumerate(shapes)]
+    xs = [randn((M, K), seed=80 + i, dtype=dtype).to(DEV) for i, (N, K) in enumerate(shapes)]
+    outs = int4_hip.w4a16_matmul_grouped(xs, ws)
+    for x, (qw, s, z), y in zip(xs, ws, outs):
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+        assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), y.view(torch.int16))
