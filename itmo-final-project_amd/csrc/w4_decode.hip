@@ -57,14 +57,11 @@ struct DecArgs {
 };
 
 // M == 1 tilings (dec_kernel_one)
-constexpr int kCfgT64N8 = 0;    // 64 columns, one round of 8 loads per wave
-constexpr int kCfgT64N16 = 1;   // 64 columns, one round of 16 loads
-constexpr int kCfgT64Ring = 2;  // 64 columns, rounds of 8 loads, two in flight
-constexpr int kCfgT32N16 = 3;   // 32 columns, one round of 16 loads
-constexpr int kCfgT32Ring = 4;  // 32 columns, rounds of 8 loads, two in flight
-constexpr int kCfgVec4 = 5;     // generic path (unaligned scales or N % 8 != 0)
-constexpr int kCfgVec2 = 6;
-constexpr int kCfgVec1 = 7;
+constexpr int kCfgT128 = 0;     // 128 columns, one round of 8 loads per wave (K <= 2048)
+constexpr int kCfgT64 = 1;      // 64 columns, one round (K <= 4096)
+constexpr int kCfgT64Ring = 2;  // 64 columns, rounds of 4 loads, two in flight (group 32, long K)
+constexpr int kCfgT32 = 3;      // 32 columns, one round (K <= 8192)
+constexpr int kCfgT32Ring = 4;  // 32 columns, rounds of 4 loads, two in flight (K > 8192)
 
 struct DecGroupedArgs {
   DecArgs prob[W4_MAX_GROUPED];
@@ -377,51 +374,78 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
 
 // ---------------------------------------------------------------- M == 1 path
 //
-// Every wave issues all loads of a round (NL 128-bit weight loads per lane,
-// plus one or two loads each for the round's activations, scales and zeros)
-// before it waits for any of them; with NL = 8 or 16 a round is a wave's
-// whole run for the common shapes, so a workgroup exposes one memory latency.
+// One workgroup of 16 waves per CU-sized unit of work: a column tile over the
+// whole K of about 128 KB of packed weights, so that the seven linears of a
+// decoder block become about 230 equal workgroups, at most one per CU.  Every
+// wave issues all loads of its run (a round of NL 128-bit weight loads per
+// lane, plus one load each for the round's activations, scales and zeros)
+// before it waits for any of them; for K <= 8192 a round is the whole run, so
+// a workgroup exposes one memory latency.
 //
-// Column tiles (always four columns per lane, 128-bit weight loads):
-//   T64: 64 columns; lane l = (quad c = l % 16, row kb = l / 16): a load step
-//        covers 4 qweight rows (32 k) x 256 bytes.
-//   T32: 32 columns; lane l = (quad c = l % 8, row r = l / 8): a load step
-//        covers 8 qweight rows (64 k) x 128 bytes (one cache line a row).  In
-//        the 16x16x32 MFMA, lanes l and l + 8 share a k slice but carry
-//        different rows, so row 0 / column n < 8 of the result sums the even
-//        rows and row 8 / column n + 8 the odd rows of quad n; each half is
-//        corrected with its own activation sum and the halves are added in
-//        the final reduction.
+// Column tiles (four columns per lane, 128-bit weight loads, rows read in
+// full 128-byte lines or longer):
+//   T128 (K <= 2048): lane l = (quad l % 32, row l / 32); a load step covers
+//        2 qweight rows (16 k) x 512 bytes.  In the 16x16x32 MFMA the four
+//        k slices are (row, column half) = (0,0) (0,1) (1,0) (1,1); the A
+//        operand of rows m < 8 is zero in the odd slices and that of rows
+//        m >= 8 in the even slices, so row 0 of the result holds columns
+//        0..63 and row 8 columns 64..127.
+//   T64  (K <= 4096): lane l = (quad l % 16, row l / 16); 4 rows (32 k) x 256
+//        bytes per step; all A rows equal, row 0 holds the 64 columns.
+//   T32  (longer K): lane l = (quad l % 8, row l / 8); 8 rows (64 k) x 128
+//        bytes per step.  Lanes l and l + 8 share a k slice but carry
+//        different rows, so row 0 / columns 0..7 of the result sums the even
+//        rows and row 8 / columns 8..15 the odd rows; the two halves are
+//        corrected with their own activation sums and added in the final
+//        reduction.
 // Activations (permuted to the nibble order), scales and zeros are staged in
 // a per-wave LDS area that only the wave itself reads (no barrier).
-constexpr int kOneWaveLds = 6144;  // per wave: activations 2 KB, scales 2 KB, zeros 2 KB
-constexpr int kOneRedOffset = kDecWaves * kOneWaveLds;
+constexpr int kOneWaves = 16;
+constexpr int kOneThreads = 64 * kOneWaves;
+constexpr int kOneWaveLds = 3072;  // per wave: activations 1 KB, scales 1 KB, zeros 1 KB
+constexpr int kOneRedOffset = kOneWaves * kOneWaveLds;
+constexpr int kOneLds = kOneRedOffset + kOneWaves * 128 * (int)sizeof(float);
 
-template <int DT, int TILE, int GSI, int NL, int D>
+template <int DT, int TW, int GSI, int NL, int D>
 __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t* lds) {
   typedef typename Act<DT>::frag F;
   typedef DecNum<DT> Num;
-  constexpr bool T32 = TILE == 32;
-  constexpr int SK = T32 ? 64 : 32;          // k per load step
-  constexpr int RPS = SK / 8;                // qweight rows per load step
-  constexpr int GS = GSI < NL ? GSI : NL;    // correction interval (steps)
-  constexpr int NP = NL / GS;                // correction points = staged groups per round
-  constexpr int LPG = TILE * 2 / 16;         // lanes per staged group row (16 B each)
-  constexpr int SZL = (NP * LPG + 63) / 64;  // scale (and zero) loads per round
-  constexpr int XE = NL * RPS;               // activation entries (8 k) per round
-  constexpr int XL = (XE + 63) / 64;         // activation loads per round
-  static_assert(XE * 16 <= 2048 && SZL * 1024 <= 2048, "per-wave LDS area");
+  constexpr int RPS = TW == 128 ? 2 : TW == 64 ? 4 : 8;  // qweight rows per load step
+  constexpr int SK = 8 * RPS;                            // k per load step
+  constexpr int SLOTS = RPS < 4 ? 4 : RPS;               // LDS activation slots per step
+  constexpr int QPR = TW / 4;                            // lanes per qweight row
+  constexpr int GS = GSI < NL ? GSI : NL;                // correction interval (steps)
+  constexpr int NP = NL / GS;                            // correction points = staged groups
+  constexpr int LPG = TW / 8;                            // lanes per staged group row (16 B)
+  constexpr int XE = NL * RPS;                           // activation entries (8 k) per round
+  static_assert(XE <= 64 && NP * LPG <= 64 && NL * SLOTS * 16 <= 1024, "per-wave staging area");
   static_assert(GSI >= 1 && (NL % GS) == 0, "correction interval");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int cq = T32 ? (lane & 7) : (lane & 15);
-  const int rr = T32 ? (lane >> 3) : (lane >> 4);
+  const int lq = lane % QPR, lr = lane / QPR;  // load quad and row within a step
+  // A-operand slot within a step (T128: slots 2 and 3 stay zero)
+  int a_slot = lr;
+  if constexpr (TW == 128) a_slot = (((lane & 15) >> 3) == ((lane >> 4) & 1)) ? (lane >> 5) : 2;
+  // result owners: output quad oq (columns 4 oq .. 4 oq + 3) and part
+  bool owner;
+  int oq, part = 0;
+  if constexpr (TW == 128) {
+    owner = lane < 16 || (lane >= 32 && lane < 48);
+    oq = lane < 32 ? (lane & 15) : 16 + (lane & 15);
+  } else if constexpr (TW == 64) {
+    owner = lane < 16;
+    oq = lane & 15;
+  } else {
+    owner = lane < 8 || (lane >= 40 && lane < 48);
+    oq = lane & 7;
+    part = lane >= 40 ? 1 : 0;
+  }
   const int N = a.N, K = a.K;
-  const int n0 = tile * TILE;
+  const int n0 = tile * TW;
   const int S = K / SK;
-  const int per_wave = ((S + kDecWaves - 1) / kDecWaves + NL - 1) / NL * NL;
+  const int per_wave = ((S + kOneWaves - 1) / kOneWaves + NL - 1) / NL * NL;
   const int wb = min(S, wv * per_wave);
   const int we = min(S, wb + per_wave);
 
@@ -435,43 +459,39 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kDecBufFlags);
 
   const uint32_t step_bytes = (uint32_t)RPS * 4u * (uint32_t)N;
-  const uint32_t w_lane = ((uint32_t)rr * (uint32_t)N + (uint32_t)(n0 + 4 * cq)) * 4u;
-  const uint32_t sz_row = (uint32_t)(lane / LPG);
-  const uint32_t sz_col = (uint32_t)(n0 * 2 + (lane % LPG) * 16);
+  const uint32_t w_lane = ((uint32_t)lr * (uint32_t)N + (uint32_t)(n0 + 4 * lq)) * 4u;
+  const uint32_t x_oob = lane < XE ? 0u : kDecOOB;
+  const uint32_t sz_oob = lane < NP * LPG ? 0u : kDecOOB;
+  const uint32_t sz_lane = (uint32_t)(lane / LPG) * (uint32_t)N * 2u + (uint32_t)(n0 * 2 + (lane % LPG) * 16);
   uint8_t* x_lds = lds + wv * kOneWaveLds;
-  uint8_t* s_lds = x_lds + 2048;
-  uint8_t* z_lds = x_lds + 4096;
+  uint8_t* s_lds = x_lds + 1024;
+  uint8_t* z_lds = x_lds + 2048;
   const uint32_t magic = dec_magic_vgpr<DT>();
   const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
+  if constexpr (TW == 128) {
+    // the zero A slots (2 and 3 of every step) are never rewritten
+    if (lane < 2 * NL)
+      *reinterpret_cast<u32x4*>(x_lds + ((lane >> 1) * SLOTS + 2 + (lane & 1)) * 16) = u32x4{0u, 0u, 0u, 0u};
+  }
 
   struct Round {
     u32x4 w[NL];
-    u32x4 x[XL];
-    u32x4 s[SZL], z[SZL];
+    u32x4 x, s, z;
   };
   // Issue order = order of use: activations, scales, zeros, weights.
   auto load_round = [&](Round& r, int sb) {
     const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < XL; ++i) {
-      const uint32_t e = (uint32_t)(lane + 64 * i);
-      const uint32_t eoob = e < (uint32_t)XE ? 0u : kDecOOB;
-      r.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (((uint32_t)sb * RPS + e) * 16u) | eoob | oob, 0, 0);
-    }
+    r.x = __builtin_amdgcn_raw_buffer_load_b128(rx, (((uint32_t)sb * RPS + (uint32_t)lane) * 16u) | x_oob | oob, 0, 0);
     const uint32_t g0 = (uint32_t)((sb * SK) >> a.gshift);
-#pragma unroll
-    for (int i = 0; i < SZL; ++i) {
-      const uint32_t gr = sz_row + (uint32_t)(64 / LPG) * i;
-      const uint32_t goob = gr < (uint32_t)NP ? 0u : kDecOOB;
-      const uint32_t off = ((g0 + gr) * (uint32_t)N * 2u + sz_col) | goob | oob;
-      r.s[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
-      r.z[i] = __builtin_amdgcn_raw_buffer_load_b128(rz, off, 0, 0);
-    }
+    const uint32_t so = (g0 * (uint32_t)N * 2u + sz_lane) | sz_oob | oob;
+    r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0);
+    r.z = __builtin_amdgcn_raw_buffer_load_b128(rz, so, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t vo = ((uint32_t)sb * step_bytes + w_lane) | oob;
 #pragma unroll
-    for (int i = 0; i < NL; ++i) r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, vo + (uint32_t)i * step_bytes, 0, 0);
+    for (int i = 0; i < NL; ++i)
+      r.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rq, vo + (uint32_t)i * step_bytes, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -479,23 +499,19 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   f32x4 xs;
   float tot[4] = {0.f, 0.f, 0.f, 0.f};
 
-  auto compute_round = [&](const Round& r) {
-    // stage this round's activations (permuted), scales and zeros
-#pragma unroll
-    for (int i = 0; i < XL; ++i)
-      *reinterpret_cast<u32x4*>(x_lds + (lane + 64 * i) * 16) = dec_perm_x(r.x[i]);
-#pragma unroll
-    for (int i = 0; i < SZL; ++i) {
-      *reinterpret_cast<u32x4*>(s_lds + (lane + 64 * i) * 16) = r.s[i];
-      *reinterpret_cast<u32x4*>(z_lds + (lane + 64 * i) * 16) = r.z[i];
-    }
+  auto compute_round = [&](const Round& r, int sb) {
+    // stage the round's activations (permuted), scales and zeros
+    if (lane < XE)
+      *reinterpret_cast<u32x4*>(x_lds + ((lane / RPS) * SLOTS + lane % RPS) * 16) = dec_perm_x(r.x);
+    *reinterpret_cast<u32x4*>(s_lds + lane * 16) = r.s;
+    *reinterpret_cast<u32x4*>(z_lds + lane * 16) = r.z;
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
 #pragma unroll
       for (int i = 0; i < GS; ++i) {
         const int st = p * GS + i;
-        const F xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(x_lds + (st * RPS + rr) * 16));
+        const F xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(x_lds + (st * SLOTS + a_slot) * 16));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const F b = __builtin_bit_cast(F, Num::bvals(r.w[st][j], magic));
@@ -503,9 +519,10 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
         }
         xs = Mfma<DT>::m16(xa, ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs);
       }
-      const int gp = (p * GS * SK) >> a.gshift;  // staged group row of this point
-      const u32x2 sv = *reinterpret_cast<const u32x2*>(s_lds + gp * TILE * 2 + cq * 8);
-      const u32x2 zv = *reinterpret_cast<const u32x2*>(z_lds + gp * TILE * 2 + cq * 8);
+      // staged group row of this point (the first staged row is the group of sb)
+      const int gp = ((sb + p * GS) * SK >> a.gshift) - ((sb * SK) >> a.gshift);
+      const u32x2 sv = *reinterpret_cast<const u32x2*>(s_lds + gp * TW * 2 + oq * 8);
+      const u32x2 zv = *reinterpret_cast<const u32x2*>(z_lds + gp * TW * 2 + oq * 8);
       const float ox = Num::OFF * xs[0];
       const float qx = Num::QS * xs[0];
 #pragma unroll
@@ -524,39 +541,35 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     if (wb < we) {
       Round r;
       load_round(r, wb);
-      compute_round(r);
+      compute_round(r, wb);
     }
   } else {
     Round ra, rb;
     load_round(ra, wb);
     load_round(rb, wb + NL);
     for (int sb = wb; sb < we; sb += 2 * NL) {
-      compute_round(ra);
+      compute_round(ra, sb);
       load_round(ra, sb + 2 * NL);
-      if (sb + NL < we) compute_round(rb);
+      if (sb + NL < we) compute_round(rb, sb + NL);
       load_round(rb, sb + 3 * NL);
     }
   }
 
-  // cross-wave (and, T32, even/odd half) reduction in a fixed order
+  // cross-wave (T32: and even/odd row) reduction in a fixed order
   float* red = reinterpret_cast<float*>(lds + kOneRedOffset);
-  // T64: row 0 = lanes 0..15.  T32: row 0 / columns 0..7 = lanes 0..7 (even
-  // rows), row 8 / columns 8..15 = lanes 40..47 (odd rows).
-  const bool owner = T32 ? (lane < 8 || (lane >= 40 && lane < 48)) : lane < 16;
   if (owner) {
-    const int half = T32 && lane >= 40 ? 1 : 0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[wv * 64 + half * 32 + 4 * cq + j] = tot[j];
+    for (int j = 0; j < 4; ++j) red[wv * 128 + part * 32 + 4 * oq + j] = tot[j];
   }
   __syncthreads();
-  if (tid < TILE) {
+  if (tid < TW) {
     const int n = n0 + tid;
     if (n < N) {
       float v = 0.0f;
 #pragma unroll
-      for (int w = 0; w < kDecWaves; ++w) {
-        v += red[w * 64 + tid];
-        if constexpr (T32) v += red[w * 64 + 32 + tid];
+      for (int w = 0; w < kOneWaves; ++w) {
+        v += red[w * 128 + tid];
+        if constexpr (TW == 32) v += red[w * 128 + 32 + tid];
       }
       a.y[n] = float_to_act_bits<DT>(v * (1.0f / Num::QS));
     }
@@ -564,7 +577,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
 }
 
 template <int DT, int GC>
-__global__ __launch_bounds__(kDecThreads) void dec_kernel_one(DecGroupedArgs g) {
+__global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) {
   extern __shared__ __attribute__((aligned(16))) float dec_smem[];
   const int t = blockIdx.x;
   int p = 0;
@@ -574,18 +587,16 @@ __global__ __launch_bounds__(kDecThreads) void dec_kernel_one(DecGroupedArgs g) 
   const DecArgs& a = g.prob[p];
   const int tile = t - g.wg_start[p];
   uint8_t* lds = reinterpret_cast<uint8_t*>(dec_smem);
-  constexpr int G64 = 1 << GC;                 // steps per group, 32-k steps
-  constexpr int G32 = GC >= 1 ? (1 << (GC - 1)) : 1;  // 64-k steps (T32 needs group >= 64)
-  constexpr int GSO = G64 < 8 ? G64 : 8;       // generic-path interval
+  // steps per group (GC = log2(group / 32), 4 meaning >= 512)
+  constexpr int G128 = 2 << GC;
+  constexpr int G64 = 1 << GC;
+  constexpr int G32 = GC >= 1 ? (1 << (GC - 1)) : 1;  // the host uses T32 for groups >= 64 only
   switch (a.cfg) {
-    case kCfgT64N8: dec_tile_one<DT, 64, G64, 8, 1>(a, tile, lds); break;
-    case kCfgT64N16: dec_tile_one<DT, 64, G64, 16, 1>(a, tile, lds); break;
-    case kCfgT64Ring: dec_tile_one<DT, 64, G64, 8, 2>(a, tile, lds); break;
-    case kCfgT32N16: dec_tile_one<DT, 32, G32, 16, 1>(a, tile, lds); break;
-    case kCfgT32Ring: dec_tile_one<DT, 32, G32, 8, 2>(a, tile, lds); break;
-    case kCfgVec4: dec_tile<DT, 4, true, (GSO < 4 ? GSO : 4)>(a, tile, dec_smem + kDecWaves * 64 * 4, reinterpret_cast<uint32_t*>(dec_smem)); break;
-    case kCfgVec2: dec_tile<DT, 2, true, GSO>(a, tile, dec_smem + kDecWaves * 64 * 4, reinterpret_cast<uint32_t*>(dec_smem)); break;
-    default: dec_tile<DT, 1, true, GSO>(a, tile, dec_smem + kDecWaves * 64 * 4, reinterpret_cast<uint32_t*>(dec_smem)); break;
+    case kCfgT128: dec_tile_one<DT, 128, G128, 8, 1>(a, tile, lds); break;
+    case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1>(a, tile, lds); break;
+    case kCfgT64Ring: dec_tile_one<DT, 64, G64, 4, 2>(a, tile, lds); break;
+    case kCfgT32: dec_tile_one<DT, 32, G32, 8, 1>(a, tile, lds); break;
+    default: dec_tile_one<DT, 32, G32, 4, 2>(a, tile, lds); break;
   }
 }
 
@@ -624,7 +635,9 @@ bool dec_fits_32bit(int64_t N, int64_t K) {
 struct DecPlan {
   w4::DecGroupedArgs g;
   int wgs;
-  int gs;  // correction interval class (1, 2, 4, 8)
+  int gs;         // group-size class of the chosen kernel
+  bool cu_tiles;  // M == 1 one-workgroup-per-CU kernel (dec_kernel_one)
+  int threads;
   size_t lds;
 };
 
@@ -642,40 +655,46 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int64_t tiles, bytes_per_wg;
   } items[W4_MAX_GROUPED];
   int gclass = -1;
-  bool one_path = false;
+  bool cu_tiles = M == 1;  // every problem fits the one-workgroup-per-CU tilings
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     if (!dec_fits_32bit(q.N, q.K) || q.group_size < 32 || !is_pow2(q.group_size)) return false;
-    // M == 1: log2(G / 32) capped at 4; M > 1: min(G / 32, 8).  One class per launch.
-    const int cls = M == 1 ? std::min(ilog2(q.group_size) - 5, 4) : (int)std::min<int64_t>(q.group_size / 32, 8);
-    if (gclass >= 0 && cls != gclass) return false;
-    gclass = cls;
+    if (gclass >= 0 && ilog2(q.group_size) != ilog2(problems[0].group_size)) return false;
+    gclass = 0;
     if (((uintptr_t)q.x % 16) != 0) return false;
     if (M > 1 && ((sxm[i] % 8) != 0 || sxm[i] < q.K || ((M - 1) * sxm[i] + q.K) * 2 >= (1LL << 31))) return false;
     if (ldy != nullptr && ldy[i] < q.N) return false;
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
-    int vec = 1, cfg = w4::kCfgVec1, tn = 16;
-    if (M == 1 && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0) {
-      // one-round M == 1 tilings: 64 columns up to K = 4096, 32 columns beyond
-      const bool t32 = q.K > 4096 && q.group_size >= 64;
-      const int64_t steps = q.K / (t32 ? 64 : 32);
-      const int64_t per_wave = (steps + w4::kDecWaves - 1) / w4::kDecWaves;
-      tn = t32 ? 32 : 64;
+    cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
+  }
+  const int G = problems[0].group_size;
+  for (int i = 0; i < count; ++i) {
+    const w4a16_problem& q = problems[i];
+    const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
+    int vec = 1, cfg = 0, tn = 16;
+    if (cu_tiles) {
+      // about 128 KB of packed weights per workgroup
       vec = 4;
-      if (t32)
-        cfg = per_wave <= 16 ? w4::kCfgT32N16 : w4::kCfgT32Ring;
-      else
-        cfg = per_wave <= 8 ? w4::kCfgT64N8 : per_wave <= 16 ? w4::kCfgT64N16 : w4::kCfgT64Ring;
-      one_path = true;
+      if (q.K <= 2048) {
+        tn = 128, cfg = w4::kCfgT128;
+      } else if (q.K <= 4096 || G < 64) {
+        tn = 64, cfg = q.K <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring;
+      } else {
+        tn = 32, cfg = q.K <= 8192 ? w4::kCfgT32 : w4::kCfgT32Ring;
+      }
     } else if (q.N % 4 == 0 && qa % 16 == 0 && sa % 8 == 0 && za % 8 == 0 && q.K <= 4096) {
-      vec = 4, cfg = w4::kCfgVec4, tn = 64;
+      vec = 4, tn = 64;
     } else if (q.N % 2 == 0 && qa % 8 == 0 && sa % 4 == 0 && za % 4 == 0) {
-      vec = 2, cfg = w4::kCfgVec2, tn = 32;
+      vec = 2, tn = 32;
     }
     items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn, (int64_t)tn * q.K / 2};
   }
-  // largest workgroups first, so the longest-running ones start first
-  std::stable_sort(items, items + count, [](const Item& l, const Item& r) { return l.bytes_per_wg > r.bytes_per_wg; });
+  // Longest-running workgroups first: more bytes, then longer K (narrower
+  // tiles with more correction points per byte).
+  std::stable_sort(items, items + count, [&](const Item& l, const Item& r) {
+    if (l.bytes_per_wg != r.bytes_per_wg) return l.bytes_per_wg > r.bytes_per_wg;
+    return problems[l.idx].K > problems[r.idx].K;
+  });
   int wgs = 0;
   for (int s = 0; s < count; ++s) {
     const Item& it = items[s];
@@ -704,18 +723,22 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   for (int s = count; s <= W4_MAX_GROUPED; ++s) dp.g.wg_start[s] = wgs;
   dp.g.count = count;
   dp.wgs = wgs;
-  dp.gs = gclass;
-  if (M == 1)  // per-wave staging areas (or the generic activation slots) + reduction
-    dp.lds = (one_path ? (size_t)w4::kOneRedOffset : (size_t)w4::kDecWaves * 64 * 16) +
-             (size_t)w4::kDecWaves * 64 * sizeof(float);
-  else
-    dp.lds = (size_t)w4::kDecWaves * M * 64 * sizeof(float);
+  dp.cu_tiles = cu_tiles;
+  if (cu_tiles) {
+    dp.gs = std::min(ilog2(G) - 5, 4);  // dec_kernel_one: log2(group / 32), 4 = ">= 512"
+    dp.threads = w4::kOneThreads;
+    dp.lds = w4::kOneLds;
+  } else {
+    dp.gs = (int)std::min(G / 32, 8);  // dec_kernel: steps per group, capped at 8
+    dp.threads = w4::kDecThreads;
+    dp.lds = (M == 1 ? (size_t)w4::kDecWaves * 64 * 16 : 0) + (size_t)w4::kDecWaves * M * 64 * sizeof(float);
+  }
   return wgs > 0;
 }
 
 template <int DT>
 void dec_launch_one(const DecPlan& dp, hipStream_t st) {
-  const dim3 grid((unsigned)dp.wgs), block(w4::kDecThreads);
+  const dim3 grid((unsigned)dp.wgs), block(w4::kOneThreads);
   switch (dp.gs) {
     case 0: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 0>), grid, block, dp.lds, st, dp.g); break;
     case 1: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 1>), grid, block, dp.lds, st, dp.g); break;
@@ -725,15 +748,25 @@ void dec_launch_one(const DecPlan& dp, hipStream_t st) {
   }
 }
 
-template <int DT>
-void dec_launch_rows(const DecPlan& dp, hipStream_t st) {
+template <int DT, bool ONE>
+void dec_launch_generic(const DecPlan& dp, hipStream_t st) {
   const dim3 grid((unsigned)dp.wgs), block(w4::kDecThreads);
   switch (dp.gs) {
-    case 1: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 1>), grid, block, dp.lds, st, dp.g); break;
-    case 2: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 2>), grid, block, dp.lds, st, dp.g); break;
-    case 4: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 4>), grid, block, dp.lds, st, dp.g); break;
-    default: hipLaunchKernelGGL((w4::dec_kernel<DT, false, 8>), grid, block, dp.lds, st, dp.g); break;
+    case 1: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 1>), grid, block, dp.lds, st, dp.g); break;
+    case 2: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 2>), grid, block, dp.lds, st, dp.g); break;
+    case 4: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 4>), grid, block, dp.lds, st, dp.g); break;
+    default: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 8>), grid, block, dp.lds, st, dp.g); break;
   }
+}
+
+template <int DT>
+void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
+  if (dp.cu_tiles)
+    dec_launch_one<DT>(dp, st);
+  else if (M == 1)
+    dec_launch_generic<DT, true>(dp, st);
+  else
+    dec_launch_generic<DT, false>(dp, st);
 }
 
 }  // namespace
@@ -746,16 +779,9 @@ int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const in
                      int x_dtype, int64_t M, hipStream_t st) {
   DecPlan dp;
   if (!dec_plan(problems, sxm, ldy, count, M, dp)) return W4_ERR_UNSUPPORTED;
-  if (x_dtype == W4_DTYPE_BF16) {
-    if (M == 1)
-      dec_launch_one<W4_DTYPE_BF16>(dp, st);
-    else
-      dec_launch_rows<W4_DTYPE_BF16>(dp, st);
-  } else {
-    if (M == 1)
-      dec_launch_one<W4_DTYPE_FP16>(dp, st);
-    else
-      dec_launch_rows<W4_DTYPE_FP16>(dp, st);
-  }
+  if (x_dtype == W4_DTYPE_BF16)
+    dec_launch<W4_DTYPE_BF16>(dp, M, st);
+  else
+    dec_launch<W4_DTYPE_FP16>(dp, M, st);
   return check_launch("w4a16 decode");
 }

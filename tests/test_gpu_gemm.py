@@ -217,3 +217,21 @@ def test_decode_ragged_shapes(M, dtype, G):
     for x, (qw, s, z), y in zip(xs, ws, outs):
         _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
         assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), y.view(torch.int16))
+
+
+# M == 1 one-workgroup-per-CU tilings: 128 columns (K <= 2048, short runs at
+# K = 512), 64 columns (K = 4096, and rounds of 4 loads for group 32 at long
+# K), 32 columns (K = 6144 / 8192, rounds for K = 16384); partial last tiles;
+# group sizes from 32 to 1024 (the largest beyond the kernel's size classes)
+@pytest.mark.parametrize("G", [32, 64, 128, 1024])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_cu_tiles(dtype, G):
+    shapes = [(N, K) for N, K in [(200, 2048), (8, 512), (96, 4096), (40, 8192), (48, 6144), (16, 16384)]
+              if K % G == 0]
+    print(f"[decode-cu] G={G} {dtype} shapes={shapes}", flush=True)
+    ws = [_weights(N, K, G, seed=90 + i) for i, (N, K) in enumerate(shapes)]
+    xs = [randn((1, K), seed=100 + i, dtype=dtype).to(DEV) for i, (N, K) in enumerate(shapes)]
+    outs = int4_hip.w4a16_matmul_grouped(xs, ws)
+    for x, (qw, s, z), y in zip(xs, ws, outs):
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+        assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), y.view(torch.int16))
