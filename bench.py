@@ -137,6 +137,71 @@ def cpu_baseline(packed, xs_bits, sample_passes: int) -> dict:
             "ms_per_block": round(t * 1e3, 3)}
 
 
+PROFILE = ROOT / "profiles" / "dec_kernel_one_decode_block_m1.md"
+ROOFLINE_KERNEL = "dec_kernel_one<0, 2>"
+
+
+def summarize_prof(d: Path, kernel: str = ROOFLINE_KERNEL) -> str:
+    """Markdown lines from a rocprofv3 run directory laid out as
+    ``trace/`` (--kernel-trace --stats), ``fetch/`` (--pmc FETCH_SIZE),
+    ``write/`` (--pmc WRITE_SIZE) and optionally ``sq/``, each written with
+    ``--output-format csv -o run``.  FETCH_SIZE / WRITE_SIZE are scaled by what
+    they read for the 32 MiB device copy of ``--copy-calib``."""
+    import csv
+
+    def rows(sub, name):
+        f = d / sub / f"run_{name}.csv"
+        return list(csv.DictReader(open(f))) if f.exists() else []
+
+    def counter(sub, name, match):
+        vals = [float(r["Counter_Value"]) for r in rows(sub, "counter_collection")
+                if match(r["Kernel_Name"]) and r["Counter_Name"] == name]
+        return sum(vals) / len(vals) if vals else None
+
+    out = []
+    stats = [r for r in rows("trace", "kernel_stats") if kernel in r["Name"]]
+    dur_ns = float(stats[0]["AverageNs"]) if stats else None
+    if stats:
+        r = stats[0]
+        out.append(f"- kernel `{r['Name']}`: {r['Calls']} calls, average {float(r['AverageNs']) / 1e3:.3f} us, "
+                   f"min {float(r['MinNs']) / 1e3:.3f} us, max {float(r['MaxNs']) / 1e3:.3f} us")
+    is_copy = lambda n: "copyBuffer" in n  # noqa: E731
+    is_k = lambda n: kernel in n  # noqa: E731
+    f_copy, w_copy = counter("fetch", "FETCH_SIZE", is_copy), counter("write", "WRITE_SIZE", is_copy)
+    f_k, w_k = counter("fetch", "FETCH_SIZE", is_k), counter("write", "WRITE_SIZE", is_k)
+    traffic = None
+    if None not in (f_copy, w_copy, f_k, w_k):
+        fs, ws = 32768.0 / f_copy, 32768.0 / w_copy  # KiB actually moved by the 32 MiB copy
+        traffic = (f_k * fs + w_k * ws) * 1024
+        out.append(f"- calibration (32 MiB device copy): FETCH_SIZE {f_copy:.1f} KiB -> factor {fs:.3f}; "
+                   f"WRITE_SIZE {w_copy:.1f} KiB -> factor {ws:.3f}")
+        out.append(f"- per dispatch: FETCH_SIZE {f_k:.1f} KiB (x{fs:.3f} = {f_k * fs * 1024 / 1e6:.3f} MB), "
+                   f"WRITE_SIZE {w_k:.1f} KiB (x{ws:.3f} = {w_k * ws * 1024 / 1e6:.3f} MB)")
+        out.append(f"- traffic_bytes_per_launch: {traffic:.0f}")
+        out.append(f"- algorithmic bytes per launch: {block_bytes(1)} "
+                   f"(traffic / algorithmic = {traffic / block_bytes(1):.3f})")
+        if dur_ns:
+            out.append(f"- algorithmic rate at the traced duration: {block_bytes(1) / dur_ns:.1f} GB/s")
+    sq = {}
+    for r in rows("sq", "counter_collection"):
+        if is_k(r["Kernel_Name"]):
+            sq.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+    if sq:
+        out.append("- SQ counters per dispatch: " + ", ".join(
+            f"{k} {sum(v) / len(v):.0f}" for k, v in sorted(sq.items())))
+    return "\n".join(out)
+
+
+def profiled_traffic() -> dict | None:
+    """HBM bytes per launch of the roofline kernel, from the committed profile."""
+    if not PROFILE.exists():
+        return None
+    for line in PROFILE.read_text().splitlines():
+        if line.startswith("- traffic_bytes_per_launch:"):
+            return {"bytes": int(float(line.split(":")[1])), "source": str(PROFILE.relative_to(ROOT))}
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -144,13 +209,18 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--sets", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-passes", type=int, default=5)
+    ap.add_argument("--cpu-passes", type=int, default=30)
     ap.add_argument("--only", default="all",
                     help="comma list of sections to run: decode, perlinear, splitk, prefill, quantize "
                          "(profiling runs use one section; the JSON line needs 'decode')")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 32 MiB device copy (for scaling FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--summarize-prof", default=None, metavar="DIR",
+                    help="print the profile summary of a rocprofv3 run directory and exit (no GPU use)")
     args = ap.parse_args()
+    if args.summarize_prof:
+        print(summarize_prof(Path(args.summarize_prof)))
+        return 0
     only = set(args.only.split(",")) if args.only != "all" else {"decode", "perlinear", "splitk", "prefill", "quantize"}
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the W4A16 path has no collective); "
@@ -278,6 +348,7 @@ def main() -> int:
         packed0 = [(qw.cpu().numpy(), bits(s.cpu()), bits(z.cpu())) for qw, s, z in packed[0]]
         cpu = cpu_baseline(packed0, [bits(x.cpu()) for x in xs1[0]], args.cpu_passes)
 
+    traffic = profiled_traffic()
     out = {
         "metric": METRIC,
         "value": round(value, 2) if value is not None else None,
@@ -298,8 +369,10 @@ def main() -> int:
                    "M": 1, "group_size": G, "weight_sets": nsets, "bytes_per_step": bytes1},
         "roofline": None if achieved is None else {
             "bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "w4::gemv_grouped_kernel<0>", "kernel_us": round(kern_ms * 1e3, 3),
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic["bytes"] if traffic else None,
+            "traffic_source": traffic["source"] if traffic else None,
+            "kernel": "w4::" + ROOFLINE_KERNEL, "kernel_us": round(kern_ms * 1e3, 3),
             "kernel_time_source": kern_ms_src},
         "cpu_baseline": cpu,
         "decode_m1_per_linear_us": {k: round(v, 3) for k, v in per_lin.items()},
