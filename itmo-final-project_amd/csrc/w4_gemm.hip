@@ -20,7 +20,8 @@ int w4_gemv_grouped_launch(const w4a16_problem* problems, int count, int x_dtype
 int64_t w4_gemv_grouped_scratch_bytes(const w4a16_problem* problems, int count, int64_t M);
 int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
-                      void* y, int64_t ldy, hipStream_t st);
+                      void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
+size_t w4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 // Reference regime boundary: M <= SMALL_M = 64 uses split-K (gemm.py:17, 265).
 static constexpr int64_t kSmallM = 64;
@@ -31,9 +32,11 @@ static constexpr int64_t kDecodeM = 16;
 // arrival counters (zero before first use, left zero by every call), then
 // scratch (fp32 partial sums).
 extern "C" size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size) {
-  if (M < 1 || M > kSmallM || N < 1 || K < 8 || group_size < 8) return 0;
+  if (M < 1 || N < 1 || K < 8 || group_size < 8) return 0;
   size_t scratch;
-  if (M <= kDecodeM) {
+  if (M > kSmallM) {
+    scratch = w4_prefill_workspace_bytes(M, N, K);
+  } else if (M <= kDecodeM) {
     scratch = w4_gemv_workspace_bytes(M, N, K, group_size);
   } else {
     const size_t a = w4_skinny_workspace_bytes(M, N, K, (N % 4) == 0);
@@ -86,7 +89,7 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
     return w4_skinny_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y,
                             ldy, scratch, scratch_bytes, st);
   return w4_prefill_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
-                           st);
+                           scratch, scratch_bytes, st);
 }
 
 static int check_grouped(const w4a16_problem* problems, int count, int64_t M) {

@@ -16,6 +16,8 @@
 //    registers while the current step's MFMAs run.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "w4_common.hpp"
 
 namespace w4 {
@@ -184,13 +186,312 @@ __global__ __launch_bounds__(PF_WAVES * 64) void prefill_kernel(PrefillArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// pf2_kernel: dense-row prefill (the common case).
+//
+//  * 128-row tiles; NW waves side by side along N, each owning a 128 x 64
+//    output block (4 x 2 blocks of v_mfma_f32_32x32x16, 128 accumulators a
+//    lane).  Waves never share columns, so every weight is dequantized once
+//    per 128 rows and the dequantization VALU work is about half the MFMA
+//    time; registers stay within 256 a lane so two waves share each SIMD and
+//    one wave's dequantization overlaps the other's matrix work.
+//  * Packed weights: one 64-bit buffer load gives a lane two adjacent
+//    columns of one k8 row (32 lanes read a 256-byte row segment); block nb of
+//    the wave holds the columns of parity nb, so the B operand of a lane is
+//    one packed word, dequantized exactly in registers (w4_common.hpp).
+//  * Activations: 128 x 64 bf16/fp16 tile per K step through double-buffered
+//    LDS (rows padded to 72 elements), read as MFMA A fragments.
+//  * Split-K (small M): split s covers K steps [s*T, (s+1)*T) and writes fp32
+//    partials [S][M][N], summed in split order by splitk_reduce_kernel; one
+//    split writes y directly.
+//  * Loads for step t+1 are issued (activations first) before step t is
+//    computed; registers ping-pong between two sets, so no copy waits.
+struct Pf2Args {
+  const uint16_t* x;
+  const uint32_t* qw;
+  const uint16_t* sc;
+  const uint16_t* ze;
+  uint16_t* y;
+  float* ws;
+  int64_t sxm, ldy;
+  uint32_t x_bytes, qw_bytes, sz_bytes;
+  int M, N, K, gshift;
+  int tiles_n, tiles_mn, kt_per_split;
+};
+
+constexpr int PF2_BM = 128;
+constexpr int PF2_BK = 64;
+constexpr int PF2_XLD = PF2_BK + 8;
+
+template <int DT, int NW, bool SZK>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf2_kernel(Pf2Args a) {
+  typedef typename Act<DT>::frag F;
+  constexpr int NT = NW * 64;
+  constexpr int XCH = PF2_BM * PF2_BK / 8 / NT;  // 16-byte activation chunks per thread per step
+  constexpr int NSZ = SZK ? 4 : 1;                // scale/zero loads per step (per ks when group < 64)
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][PF2_BM * PF2_XLD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int t = blockIdx.x;
+  const int split = t / a.tiles_mn;
+  const int tmn = t - split * a.tiles_mn;
+  const int tile_m = tmn / a.tiles_n;
+  const int tile_n = tmn - tile_m * a.tiles_n;
+  const int m0 = tile_m * PF2_BM;
+  const int n0w = (tile_n * NW + wn) * 64;
+  const int N = a.N;
+  const int KT = (a.K + PF2_BK - 1) / PF2_BK;
+  const int kt0 = split * a.kt_per_split;
+  const int kt1 = min(kt0 + a.kt_per_split, KT);
+
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, 0x00020000);
+  constexpr uint32_t OOB = 0x80000000u;
+
+  // activation chunk c = tid + i*NT: row c / 8, k offset (c % 8) * 8
+  uint32_t x_row_off[XCH];
+  int x_kc[XCH];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int c = tid + i * NT;
+    const int m = m0 + (c >> 3);
+    x_kc[i] = (c & 7) * 8;
+    x_row_off[i] = m < a.M ? (uint32_t)((int64_t)m * a.sxm * 2) : OOB;
+  }
+  const uint32_t w_lane = ((uint32_t)lh * (uint32_t)N + (uint32_t)(n0w + 2 * l32)) * 4u;
+  const uint32_t sz_col = (uint32_t)(n0w + 2 * l32) * 2u;
+  const uint32_t magic = fp16_magic_vgpr();
+
+  struct Stage {
+    u32x4 x[XCH];
+    u32x2 w[4];
+    uint32_t s[NSZ], z[NSZ];
+  };
+  // Out-of-range offsets are OR-ed masks (bit 31), never selects between
+  // offsets, so no load ends up behind a branch.
+  auto load = [&](Stage& st, int kt) {
+    const uint32_t lmask = kt < kt1 ? 0u : OOB;  // scalar
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int k = kt * PF2_BK + x_kc[i];
+      const uint32_t kmask = (uint32_t)((a.K - 1 - k) >> 31) & OOB;  // k >= K (rows are dense)
+      st.x[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, (x_row_off[i] + (uint32_t)k * 2u) | kmask | lmask, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NSZ; ++j) {
+      const uint32_t g = (uint32_t)((kt * PF2_BK + (SZK ? j * 16 + lh * 8 : 0)) >> a.gshift);
+      const uint32_t off = (g * (uint32_t)N * 2u + sz_col) | lmask;
+      st.s[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+      st.z[j] = __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0);
+    }
+    const uint32_t wo = ((uint32_t)kt * 8u * (uint32_t)N * 4u + w_lane) | lmask;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      st.w[ks] = __builtin_amdgcn_raw_buffer_load_b64(rq, wo + (uint32_t)ks * 2u * (uint32_t)N * 4u, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto store_x = [&](const Stage& st, int buf) {
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int c = tid + i * NT;
+      *reinterpret_cast<u32x4*>(&xs[buf][(c >> 3) * PF2_XLD + x_kc[i]]) = st.x[i];
+    }
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
+
+  auto compute = [&](const Stage& st, int buf) {
+    const uint16_t* xb = xs[buf];
+    GroupConst gc[2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks == 0 || SZK) {
+        const int j = SZK ? ks : 0;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          gc[nb] = make_group_const((uint16_t)(st.s[j] >> (16 * nb)), (uint16_t)(st.z[j] >> (16 * nb)));
+      }
+      F af[4], bf[2];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        af[mb] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(&xb[(mb * 32 + l32) * PF2_XLD + ks * 16 + lh * 8]));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) bf[nb] = dequant_word<DT>(st.w[ks][nb], gc[nb], magic);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Mfma<DT>::m32(af[mb], bf[nb], acc[mb][nb]);
+    }
+  };
+
+  // Two register stages ping-pong; step t is computed from LDS buffer t & 1.
+  Stage sa, sb;
+  load(sa, kt0);
+  store_x(sa, 0);
+  load(sb, kt0 + 1);
+  __syncthreads();
+  for (int kt = kt0; kt < kt1; kt += 2) {
+    compute(sa, 0);
+    if (kt + 1 < kt1) store_x(sb, 1);
+    load(sa, kt + 2);
+    __syncthreads();
+    if (kt + 1 < kt1) compute(sb, 1);
+    store_x(sa, 0);
+    load(sb, kt + 3);
+    __syncthreads();
+  }
+
+  // epilogue: D[row][col] of a 32x32 block in lane (col + 32*h), register r,
+  // row = 8*(r/4) + 4*h + (r%4); column n0w + 2*col + nb
+  const int n = n0w + 2 * l32;
+  if (n < N) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + mb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m >= a.M) continue;
+        if (a.ws != nullptr) {
+          float2 v;
+          v.x = acc[mb][0][r];
+          v.y = acc[mb][1][r];
+          *reinterpret_cast<float2*>(a.ws + ((int64_t)split * a.M + m) * N + n) = v;
+        } else {
+          const uint32_t v = (uint32_t)float_to_act_bits<DT>(acc[mb][0][r]) |
+                             ((uint32_t)float_to_act_bits<DT>(acc[mb][1][r]) << 16);
+          *reinterpret_cast<uint32_t*>(a.y + (int64_t)m * a.ldy + n) = v;
+        }
+      }
+  }
+}
+
 }  // namespace w4
 
 using namespace w4host;
 
+namespace {
+
+struct Pf2Plan {
+  int nw = 0, splits = 1, kt_per_split = 0, tiles_n = 0, tiles_mn = 0;
+  size_t ws = 0;
+};
+
+// Static launch table (pure function of the shape and the CU count).  Cost
+// model: MFMA work spread over min(waves, 4 * CUs) SIMDs, plus the fp32
+// partials written and re-read at HBM speed and one more launch when split.
+Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K) {
+  const int cus = device_cu_count();
+  const int64_t KT = (K + w4::PF2_BK - 1) / w4::PF2_BK;
+  const int64_t tm = (M + w4::PF2_BM - 1) / w4::PF2_BM;
+  const double flops = 2.0 * (double)M * (double)N * (double)K;
+  const double simd_rate = 1024.0 * 2.4e9 * 0.6;  // flop/s of one SIMD at a sustained 60 %
+  Pf2Plan best;
+  double best_t = 1e30;
+  for (int nw : {4, 2}) {
+    const int64_t tn = (N + 64 * nw - 1) / (64 * nw);
+    for (int s : {1, 2, 4, 8}) {
+      const int64_t T = (KT + s - 1) / s;
+      const int64_t S = (KT + T - 1) / T;
+      if (S != s || (s > 1 && T < 4)) continue;
+      const double waves = (double)(tm * tn * S * nw);
+      const double simds = std::min(waves, 4.0 * cus);
+      double t = flops / (simds * simd_rate);
+      if (S > 1) t += 2.0 * (double)S * M * N * 4 / 5e12 + 2e-6;
+      if (t < best_t * 0.97) {
+        best_t = t;
+        best.nw = nw;
+        best.splits = (int)S;
+        best.kt_per_split = (int)T;
+        best.tiles_n = (int)tn;
+        best.tiles_mn = (int)(tm * tn);
+        best.ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+      }
+    }
+  }
+  return best;
+}
+
+bool pf2_ok(const void* x, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk, const void* qw,
+            const void* sc, const void* ze, const void* y, int64_t ldy) {
+  return sxk == 1 && (uintptr_t)x % 16 == 0 && sxm % 8 == 0 && N % 2 == 0 && (uintptr_t)qw % 8 == 0 &&
+         (uintptr_t)sc % 4 == 0 && (uintptr_t)ze % 4 == 0 && (uintptr_t)y % 4 == 0 && ldy % 2 == 0 &&
+         M < (1LL << 30) && ((M - 1) * sxm + K) * 2 < (1LL << 31) && (K / 8) * N * 4 < (1LL << 31);
+}
+
+template <int DT, int NW>
+void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t st) {
+  const dim3 grid((unsigned)(p.tiles_mn * p.splits)), block(NW * 64);
+  if (szk)
+    hipLaunchKernelGGL((w4::pf2_kernel<DT, NW, true>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((w4::pf2_kernel<DT, NW, false>), grid, block, 0, st, a);
+}
+
+}  // namespace
+
+int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_dtype, void* y, int64_t ldy,
+                            hipStream_t st);
+
+// Scratch bytes (past the workspace's counter area) of a prefill launch.
+size_t w4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K) { return plan_pf2(M, N, K).ws; }
+
 int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
-                      void* y, int64_t ldy, hipStream_t st) {
+                      void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (pf2_ok(x, M, N, K, sxm, sxk, qw, sc, ze, y, ldy)) {
+    const Pf2Plan p = plan_pf2(M, N, K);
+    if (p.ws > 0 && (ws == nullptr || ws_bytes < p.ws))
+      return fail(W4_ERR_WORKSPACE, "w4a16_gemm: workspace of %zu bytes required, %zu given",
+                  (size_t)W4_WORKSPACE_COUNTER_BYTES + p.ws, ws ? ws_bytes : (size_t)0);
+    w4::Pf2Args a{};
+    a.x = static_cast<const uint16_t*>(x);
+    a.qw = reinterpret_cast<const uint32_t*>(qw);
+    a.sc = sc;
+    a.ze = ze;
+    a.y = static_cast<uint16_t*>(y);
+    a.ws = p.splits > 1 ? static_cast<float*>(ws) : nullptr;
+    a.sxm = sxm;
+    a.ldy = ldy;
+    a.x_bytes = (uint32_t)(((M - 1) * sxm + K) * 2);
+    a.qw_bytes = (uint32_t)((K / 8) * N * 4);
+    a.sz_bytes = (uint32_t)((K / G) * N * 2);
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.gshift = ilog2(G);
+    a.tiles_n = p.tiles_n;
+    a.tiles_mn = p.tiles_mn;
+    a.kt_per_split = p.kt_per_split;
+    const bool szk = G < 64;
+    if (x_dtype == W4_DTYPE_BF16) {
+      if (p.nw == 4)
+        pf2_launch_g<W4_DTYPE_BF16, 4>(p, szk, a, st);
+      else
+        pf2_launch_g<W4_DTYPE_BF16, 2>(p, szk, a, st);
+    } else {
+      if (p.nw == 4)
+        pf2_launch_g<W4_DTYPE_FP16, 4>(p, szk, a, st);
+      else
+        pf2_launch_g<W4_DTYPE_FP16, 2>(p, szk, a, st);
+    }
+    int rc = check_launch("w4a16_gemm (prefill)");
+    if (rc != W4_OK || p.splits == 1) return rc;
+    return w4_splitk_reduce_launch(static_cast<const float*>(ws), p.splits, M, N, x_dtype, y, ldy, st);
+  }
+  // strided / unaligned activations: the general tile kernel
   w4::PrefillArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.sxm = sxm;

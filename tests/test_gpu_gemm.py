@@ -235,3 +235,29 @@ def test_decode_cu_tiles(dtype, G):
     for x, (qw, s, z), y in zip(xs, ws, outs):
         _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
         assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), y.view(torch.int16))
+
+
+# prefill (M > 64) on dense rows: split-K with fp32 partials for small M x N,
+# partial row tiles, every group-size path (per-lane groups below 64)
+@pytest.mark.parametrize("G", [8, 32, 64, 256])
+@pytest.mark.parametrize("M", [65, 130])
+def test_prefill_group_sizes_and_partial_tiles(M, G):
+    N, K = 96, 512
+    print(f"[prefill] M={M} N={N} K={K} G={G}", flush=True)
+    qw, s, z = _weights(N, K, G, seed=200 + G)
+    x = randn((M, K), seed=201 + M).to(DEV)
+    out = int4_hip.w4a16_matmul(x, qw, s, z)
+    _check(out, x, qw, s, z)
+
+
+@pytest.mark.parametrize("M", [128, 512])
+@pytest.mark.parametrize("NK", [(512, 2048), (2048, 8192)])
+def test_prefill_split_k_bit_identical(M, NK):
+    N, K = NK
+    print(f"[prefill-split] M={M} N={N} K={K}", flush=True)
+    qw, s, z = _weights(N, K, 128, seed=N + M)
+    x = randn((M, K), seed=300 + M, dtype=torch.float16).to(DEV)
+    out = int4_hip.w4a16_matmul(x, qw, s, z)
+    _check(out, x, qw, s, z, ref_unrounded=False)
+    for _ in range(2):
+        assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
