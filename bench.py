@@ -328,15 +328,21 @@ def main() -> int:
             msM = time_graph(gp, 10, stream)
             pre[M] = {"us_per_block": round(msM * 1e3, 2), "tflops": round(block_flops(M) / (msM * 1e-3) / 1e12, 2)}
             del gp
-            if M == 2048:
-                w_deq = [int4_hip.dequantize_int4(*packed[0][j], torch.bfloat16) for j in range(len(LINEARS))]
-                gb = graph_of(lambda: [torch.nn.functional.linear(xsM[j], w_deq[j]) for j in range(len(LINEARS))],
-                              stream)
-                time_graph(gb, 3, stream)
-                msb = time_graph(gb, 10, stream)
-                pre[M]["hipblaslt_bf16_dequantized_us"] = round(msb * 1e3, 2)
-                pre[M]["hipblaslt_bf16_tflops"] = round(block_flops(M) / (msb * 1e-3) / 1e12, 2)
-                del gb, w_deq
+            per = {}
+            for j, (name, N, K) in enumerate(LINEARS):
+                gj = graph_of(lambda j=j: [int4_hip.w4a16_matmul(xsM[j], *packed[0][j]) for _ in range(4)], stream)
+                time_graph(gj, 2, stream)
+                per[name] = round(time_graph(gj, 10, stream) / 4 * 1e3, 2)
+                del gj
+            pre[M]["per_linear_us"] = per
+            w_deq = [int4_hip.dequantize_int4(*packed[0][j], torch.bfloat16) for j in range(len(LINEARS))]
+            gb = graph_of(lambda: [torch.nn.functional.linear(xsM[j], w_deq[j]) for j in range(len(LINEARS))],
+                          stream)
+            time_graph(gb, 3, stream)
+            msb = time_graph(gb, 10, stream)
+            pre[M]["hipblaslt_bf16_dequantized_us"] = round(msb * 1e3, 2)
+            pre[M]["hipblaslt_bf16_tflops"] = round(block_flops(M) / (msb * 1e-3) / 1e12, 2)
+            del gb, w_deq
             del xsM
     torch.cuda.synchronize()
 

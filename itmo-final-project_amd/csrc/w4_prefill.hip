@@ -378,6 +378,188 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
 }
 
+// ---------------------------------------------------------------------------
+// pf3_kernel: pf2's tiling with a deeper pipeline (K a multiple of 64).
+//
+//  * Activation tiles go straight from memory to LDS (128-bit direct-to-LDS
+//    buffer loads: lane l of a load lands at base + 16 l), three K steps in a
+//    ring, so they need no staging registers.  LDS chunk (row, c) of 16 bytes
+//    sits at position row * 8 + (c ^ ((row >> 1) & 7)): the 16 lanes that a
+//    128-bit LDS read serves together (16 consecutive rows, one chunk each)
+//    then cover all 64 banks (two 128-byte rows per bank line), so the
+//    A-fragment reads are free of bank conflicts without padding.
+//  * Weights and scales/zeros rotate through three register sets.
+//  * Loads run two K steps ahead.  Every step issues the same number of
+//    loads, so "this wave's activations of step t have landed" is one fixed
+//    s_waitcnt vmcnt(N); a raw s_barrier then makes all waves' chunks
+//    visible (and frees the slot of step t - 1 for step t + 2).  The barrier
+//    is written without a memory fence because the fence would wait for every
+//    outstanding load, including the prefetched ones.
+// 16 bytes per lane from a raw buffer straight into LDS at lds + 16 * lane.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+}
+
+template <int DT, int NW, bool SZK>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_kernel(Pf2Args a) {
+  typedef typename Act<DT>::frag F;
+  constexpr int XL = 16 / NW;        // direct-to-LDS activation loads per wave per step (1 KB each)
+  constexpr int NSZ = SZK ? 4 : 1;   // scale (and zero) loads per step
+  constexpr int LPS = XL + 2 * NSZ + 4;  // loads per step and wave
+  constexpr int WAITN = 2 * NSZ + 4 + LPS;  // loads issued after a step's activation loads
+  constexpr int WAIT_IMM = (WAITN & 15) | 0x70 | 0xF00 | ((WAITN >> 4) << 14);
+  static_assert(WAITN < 64, "vmcnt range");
+  __shared__ __attribute__((aligned(16))) uint16_t xs[3][PF2_BM * PF2_BK];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int t = blockIdx.x;
+  const int split = t / a.tiles_mn;
+  const int tmn = t - split * a.tiles_mn;
+  const int tile_m = tmn / a.tiles_n;
+  const int tile_n = tmn - tile_m * a.tiles_n;
+  const int m0 = tile_m * PF2_BM;
+  const int n0w = (tile_n * NW + wn) * 64;
+  const int N = a.N;
+  const int KT = a.K / PF2_BK;
+  const int kt0 = split * a.kt_per_split;
+  const int nsteps = min(a.kt_per_split, KT - kt0);
+
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, 0x00020000);
+  constexpr uint32_t OOB = 0x80000000u;
+
+  // activation loads: instruction j of this wave fills LDS positions
+  // [64 (wn XL + j), +64); lane l -> row 8 (wn XL + j) + l / 8, swizzled slot l % 8
+  uint32_t x_off[XL];
+#pragma unroll
+  for (int j = 0; j < XL; ++j) {
+    const int row = 8 * (wn * XL + j) + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    const int m = m0 + row;
+    x_off[j] = m < a.M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)c * 16u : OOB;
+  }
+  const uint32_t w_lane = ((uint32_t)lh * (uint32_t)N + (uint32_t)(n0w + 2 * l32)) * 4u;
+  const uint32_t sz_col = (uint32_t)(n0w + 2 * l32) * 2u;
+  const uint32_t magic = fp16_magic_vgpr();
+  // A-fragment read offsets (elements) for mb = 0, ks = 0: row l32, chunk lh
+  int a_off[4][4];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int row = mb * 32 + l32;
+      const int c = ks * 2 + lh;
+      a_off[mb][ks] = (row * 8 + (c ^ ((row >> 1) & 7))) * 8;
+    }
+
+  struct Regs {
+    u32x2 w[4];
+    uint32_t s[NSZ], z[NSZ];
+  };
+  auto issue = [&](Regs& r, int st) {  // step st (0-based within this split)
+    const uint32_t lmask = st < nsteps ? 0u : OOB;  // scalar
+    const int kt = kt0 + st;
+    uint16_t* slot = xs[st % 3];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < XL; ++j)
+      lds_load16(rx, slot + (wn * XL + j) * 512, (x_off[j] + (uint32_t)kt * PF2_BK * 2u) | lmask);
+#pragma unroll
+    for (int j = 0; j < NSZ; ++j) {
+      const uint32_t g = (uint32_t)((kt * PF2_BK + (SZK ? j * 16 + lh * 8 : 0)) >> a.gshift);
+      const uint32_t off = (g * (uint32_t)N * 2u + sz_col) | lmask;
+      r.s[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+      r.z[j] = __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0);
+    }
+    const uint32_t wo = ((uint32_t)kt * 8u * (uint32_t)N * 4u + w_lane) | lmask;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      r.w[ks] = __builtin_amdgcn_raw_buffer_load_b64(rq, wo + (uint32_t)ks * 2u * (uint32_t)N * 4u, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
+
+  auto compute = [&](const Regs& r, int st) {
+    const uint16_t* xb = xs[st % 3];
+    GroupConst gc[2];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks == 0 || SZK) {
+        const int j = SZK ? ks : 0;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          gc[nb] = make_group_const((uint16_t)(r.s[j] >> (16 * nb)), (uint16_t)(r.z[j] >> (16 * nb)));
+      }
+      F af[4], bf[2];
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) af[mb] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(&xb[a_off[mb][ks]]));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) bf[nb] = dequant_word<DT>(r.w[ks][nb], gc[nb], magic);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Mfma<DT>::m32(af[mb], bf[nb], acc[mb][nb]);
+    }
+  };
+  // wait for this wave's activation loads of step st, then for every wave
+  auto sync_step = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(WAIT_IMM);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  Regs r0, r1, r2;
+  issue(r0, 0);
+  issue(r1, 1);
+  for (int st = 0; st < nsteps; st += 3) {
+    sync_step();
+    issue(r2, st + 2);
+    compute(r0, st);
+    sync_step();
+    issue(r0, st + 3);
+    if (st + 1 < nsteps) compute(r1, st + 1);
+    sync_step();
+    issue(r1, st + 4);
+    if (st + 2 < nsteps) compute(r2, st + 2);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load (and no LDS write) outstanding past the loop
+
+  const int n = n0w + 2 * l32;
+  if (n < N) {
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + mb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m >= a.M) continue;
+        if (a.ws != nullptr) {
+          float2 v;
+          v.x = acc[mb][0][r];
+          v.y = acc[mb][1][r];
+          *reinterpret_cast<float2*>(a.ws + ((int64_t)split * a.M + m) * N + n) = v;
+        } else {
+          const uint32_t v = (uint32_t)float_to_act_bits<DT>(acc[mb][0][r]) |
+                             ((uint32_t)float_to_act_bits<DT>(acc[mb][1][r]) << 16);
+          *reinterpret_cast<uint32_t*>(a.y + (int64_t)m * a.ldy + n) = v;
+        }
+      }
+  }
+}
+
 }  // namespace w4
 
 using namespace w4host;
@@ -434,10 +616,16 @@ bool pf2_ok(const void* x, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t
 template <int DT, int NW>
 void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t st) {
   const dim3 grid((unsigned)(p.tiles_mn * p.splits)), block(NW * 64);
-  if (szk)
+  if (a.K % w4::PF2_BK == 0) {  // deep pipeline: whole K steps only
+    if (szk)
+      hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, true>), grid, block, 0, st, a);
+    else
+      hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, false>), grid, block, 0, st, a);
+  } else if (szk) {
     hipLaunchKernelGGL((w4::pf2_kernel<DT, NW, true>), grid, block, 0, st, a);
-  else
+  } else {
     hipLaunchKernelGGL((w4::pf2_kernel<DT, NW, false>), grid, block, 0, st, a);
+  }
 }
 
 }  // namespace

@@ -238,11 +238,16 @@ def test_decode_cu_tiles(dtype, G):
 
 
 # prefill (M > 64) on dense rows: split-K with fp32 partials for small M x N,
-# partial row tiles, every group-size path (per-lane groups below 64)
+# partial row tiles, every group-size path (per-lane groups below 64); K a
+# multiple of 64 (deep pipeline), K = 512 + 8 (register-staged pipeline), odd N
+# (general tile kernel)
 @pytest.mark.parametrize("G", [8, 32, 64, 256])
 @pytest.mark.parametrize("M", [65, 130])
-def test_prefill_group_sizes_and_partial_tiles(M, G):
-    N, K = 96, 512
+@pytest.mark.parametrize("NK", [(96, 512), (96, 520), (73, 512)])
+def test_prefill_group_sizes_and_partial_tiles(M, G, NK):
+    N, K = NK
+    if K % G:
+        pytest.skip("group size must divide K")
     print(f"[prefill] M={M} N={N} K={K} G={G}", flush=True)
     qw, s, z = _weights(N, K, G, seed=200 + G)
     x = randn((M, K), seed=201 + M).to(DEV)
