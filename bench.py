@@ -307,15 +307,38 @@ def main() -> int:
         ms7 = time_graph(g7, 10, stream) / nsets
         del g7
 
-    # ------------------------------------------------- split-K M=16 block
-    ms16 = None
+    # ------------------------------------------------- small-M regime
+    # M in {2..64} x G in {128, 64, 32}, per-linear launches over the rotated
+    # weight sets (G=128 reuses the decode sets; G=64/32 are quantized here)
+    ms16, small = None, {}
     if "splitk" in only:
-        xs16 = [torch.randn((16, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
-        g16 = graph_of(lambda: [int4_hip.w4a16_matmul(xs16[j], *packed[i][j]) for i in range(nsets)
-                                for j in range(len(LINEARS))], stream)
-        time_graph(g16, 2, stream)
-        ms16 = time_graph(g16, 5, stream) / nsets
-        del g16
+        for g in (128, 64, 32):
+            if g == G:
+                packs = packed
+            else:
+                packs = []
+                for _ in range(nsets):
+                    one = []
+                    for _, N, K in LINEARS:
+                        w = (torch.randn((N, K), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+                        one.append(int4_hip.quantize_int4(w, g))
+                        del w
+                    packs.append(one)
+            small[g] = {}
+            for M in (2, 4, 8, 16, 32, 64):
+                xsm = [torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
+                gm = graph_of(lambda: [int4_hip.w4a16_matmul(xsm[j], *packs[i][j]) for i in range(nsets)
+                                       for j in range(len(LINEARS))], stream)
+                time_graph(gm, 2, stream)
+                msm = time_graph(gm, 5, stream) / nsets
+                small[g][M] = {"us_per_block": round(msm * 1e3, 2),
+                               "gbps": round(block_bytes(M, g) / (msm * 1e-3) / 1e9, 1)}
+                if g == G and M == 16:
+                    ms16 = msm
+                del gm, xsm
+            if g != G:
+                del packs
+            torch.cuda.empty_cache()
 
     # ------------------------------------------------- prefill M=128/512/2048
     pre = {}
@@ -384,6 +407,7 @@ def main() -> int:
         "decode_m1_per_linear_us": {k: round(v, 3) for k, v in per_lin.items()},
         "decode_m1_7_launches_us_per_block": round(ms7 * 1e3, 3) if ms7 else None,
         "decode_m1_7_launches_gbps": round(bytes1 / (ms7 * 1e-3) / 1e9, 1) if ms7 else None,
+        "small_m_7_launches": {f"G{g}": {f"M{m}": v for m, v in d.items()} for g, d in small.items()},
         "splitk_m16_us_per_block": round(ms16 * 1e3, 3) if ms16 else None,
         "splitk_m16_gbps": round(block_bytes(16) / (ms16 * 1e-3) / 1e9, 1) if ms16 else None,
         "prefill": {str(k): v for k, v in pre.items()},

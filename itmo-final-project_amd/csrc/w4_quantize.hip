@@ -54,6 +54,43 @@ __device__ __forceinline__ uint32_t quantize_pack8(const float v[8], QStats st) 
   return word;
 }
 
+// Fast form of quantize_pack8 for finite weights and a finite nonzero scale
+// (group_stats' scale is then in [2^-24, 65504]).  floor(w/scale + 0.5) is
+// taken from the reciprocal product w * rcp(scale): v_rcp_f32 is within 1 ulp,
+// so |w*rcp - w/scale| <= |w/scale| * 2^-22 and, for |w/scale| < 16.0001,
+// fl(fl(w*rcp) + 0.5) lies within 6e-6 of fl(fl(w/scale) + 0.5).  Both then
+// have the same floor unless that value is within 2^-15 of an integer.
+// *exact is nonzero when some element is, or has |w*rcp| not below 16; the
+// caller then repacks the word with quantize_pack8.  Otherwise the word is
+// bit-identical to quantize_pack8's.
+__device__ __forceinline__ uint32_t quantize_pack8_fast(const float v[8], QStats st, float rcp, uint32_t* exact) {
+#pragma clang fp contract(off)
+  constexpr float EPS = 1.0f / 32768.0f;
+  uint32_t word = 0, flag = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float r = v[i] * rcp;
+    const float t = r + 0.5f;
+    const float f = floorf(t);
+    const float d = t - f;
+    flag |= (uint32_t)(!(fabsf(r) < 16.0f) || d < EPS || d > 1.0f - EPS) << i;
+    const float qf = fminf(fmaxf(f + st.zero, 0.0f), 15.0f);
+    word += (uint32_t)(int)qf << (4 * i);
+  }
+  *exact = flag;
+  return word;
+}
+
+// The eight activation-dtype weights of one 16-byte row segment, as floats.
+template <int DT>
+__device__ __forceinline__ void unpack_row8(const u32x4 r, float v[8]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    v[2 * j] = act_bits_to_float((uint16_t)(r[j] & 0xFFFFu), DT);
+    v[2 * j + 1] = act_bits_to_float((uint16_t)(r[j] >> 16), DT);
+  }
+}
+
 // Stored fp16 patterns.  A NaN zero point is written as 0xFE00, the x86
 // "default NaN" that the reference's CPU path produces for -0/0 and for
 // negated NaN inputs; a NaN scale (NaN weights) as 0x7E00.
@@ -105,35 +142,99 @@ __global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
   const int seg = lane % L;
   const int rsub = lane / L;
 
+  // Rows are loaded in batches of up to 16 per lane before any is used, so a
+  // wave keeps 16 row segments in flight instead of one.
+  constexpr int IT = QROWS / RPI;
+  constexpr int B = IT < 16 ? IT : 16;
+  const uint32_t w_bytes = VEC ? (uint32_t)(((N - 1) * swn + K) * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t rw =
+      __builtin_amdgcn_make_buffer_rsrc((void*)w, (short)0, (int)w_bytes, 0x00020000);
   if (active) {
-#pragma unroll 2
-    for (int it = 0; it < QROWS / RPI; ++it) {
-      const int row = it * RPI + rsub;
-      const int64_t n = n0 + row;
-      const bool valid = n < N;
-      float v[8];
-      if (valid) {
-        load8<DT, VEC>(w, n, g * G + seg * 8, swn, swk, v);
+    for (int b0 = 0; b0 < IT; b0 += B) {
+      u32x4 raw[B];
+#pragma unroll
+      for (int i = 0; i < B; ++i) {
+        const int row = (b0 + i) * RPI + rsub;
+        const int64_t n = n0 + row;
+        if constexpr (VEC) {
+          // rows past N read zeros (buffer range check)
+          const uint32_t off = n < N ? (uint32_t)((n * swn + g * G + seg * 8) * 2) : 0x80000000u;
+          raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+        } else {
+          uint16_t e[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) e[j] = n < N ? w[n * swn + (g * G + seg * 8 + j) * swk] : (uint16_t)0;
+          raw[i] = u32x4{e[0] | ((uint32_t)e[1] << 16), e[2] | ((uint32_t)e[3] << 16),
+                         e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
+        }
+      }
+      // One ballot per batch: without a NaN anywhere in it, plain min/max (the
+      // sign of a zero extreme does not reach group_stats' result) and the
+      // reciprocal packing, redone exactly for the rare flagged words.
+      bool has_nan = false;
+#pragma unroll
+      for (int i = 0; i < B; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          has_nan |= act_bits_to_float((uint16_t)(raw[i][j] & 0xFFFFu), DT) !=
+                     act_bits_to_float((uint16_t)(raw[i][j] & 0xFFFFu), DT);
+          has_nan |= act_bits_to_float((uint16_t)(raw[i][j] >> 16), DT) !=
+                     act_bits_to_float((uint16_t)(raw[i][j] >> 16), DT);
+        }
+      if (__builtin_amdgcn_ballot_w64(has_nan) == 0) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+          const int row = (b0 + i) * RPI + rsub;
+          float v[8];
+          unpack_row8<DT>(raw[i], v);
+          float mx = v[0], mn = v[0];
+#pragma unroll
+          for (int j = 1; j < 8; ++j) {
+            mx = fmaxf(mx, v[j]);
+            mn = fminf(mn, v[j]);
+          }
+#pragma unroll
+          for (int off = L / 2; off > 0; off >>= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+            mn = fminf(mn, __shfl_xor(mn, off, 64));
+          }
+          const QStats st = group_stats(mx, mn);
+          uint32_t flag;
+          uint32_t word = quantize_pack8_fast(v, st, __builtin_amdgcn_rcpf(st.scale), &flag);
+          // an infinite weight makes the scale infinite and fp16 rounding can
+          // make it 0: both take the exact path
+          if (!(st.scale > 0.0f && st.scale < __builtin_inff())) flag = 1;
+          if (flag != 0) word = quantize_pack8(v, st);
+          tile[wv][seg][row] = word;
+          if (seg == 0) {
+            st_s[wv][row] = scale_bits(st.scale);
+            st_z[wv][row] = zero_bits(st.zero);
+          }
+        }
       } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
-      }
-      float mx = v[0], mn = v[0];
+        for (int i = 0; i < B; ++i) {
+          const int row = (b0 + i) * RPI + rsub;
+          float v[8];
+          unpack_row8<DT>(raw[i], v);
+          float mx = v[0], mn = v[0];
 #pragma unroll
-      for (int i = 1; i < 8; ++i) {
-        mx = max_nan(mx, v[i]);
-        mn = min_nan(mn, v[i]);
-      }
+          for (int j = 1; j < 8; ++j) {
+            mx = max_nan(mx, v[j]);
+            mn = min_nan(mn, v[j]);
+          }
 #pragma unroll
-      for (int off = L / 2; off > 0; off >>= 1) {
-        mx = max_nan(mx, __shfl_xor(mx, off, 64));
-        mn = min_nan(mn, __shfl_xor(mn, off, 64));
-      }
-      const QStats st = group_stats(mx, mn);
-      tile[wv][seg][row] = quantize_pack8(v, st);
-      if (seg == 0) {
-        st_s[wv][row] = scale_bits(st.scale);
-        st_z[wv][row] = zero_bits(st.zero);
+          for (int off = L / 2; off > 0; off >>= 1) {
+            mx = max_nan(mx, __shfl_xor(mx, off, 64));
+            mn = min_nan(mn, __shfl_xor(mn, off, 64));
+          }
+          const QStats st = group_stats(mx, mn);
+          tile[wv][seg][row] = quantize_pack8(v, st);
+          if (seg == 0) {
+            st_s[wv][row] = scale_bits(st.scale);
+            st_z[wv][row] = zero_bits(st.zero);
+          }
+        }
       }
     }
   }
@@ -340,7 +441,9 @@ extern "C" int w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K, int
   if (N == 0) return W4_OK;
   if (!w || !qweight || !scales || !zeros) return fail(W4_ERR_INVALID, "w4_quantize: null pointer");
   const uint16_t* wp = static_cast<const uint16_t*>(w);
-  const bool vec = stride_wk == 1 && (stride_wn % 8) == 0 && ((uintptr_t)wp % 16) == 0;
+  // 128-bit buffer loads: dense rows, 16-byte aligned, whole tensor within 2 GiB
+  const bool vec = stride_wk == 1 && (stride_wn % 8) == 0 && ((uintptr_t)wp % 16) == 0 &&
+                   ((N - 1) * stride_wn + K) * 2 < (1LL << 31);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (w_dtype == W4_DTYPE_BF16) {
     if (vec) launch_quantize<W4_DTYPE_BF16, true>(wp, N, K, stride_wn, stride_wk, (int)G, qweight, scales, zeros, st);

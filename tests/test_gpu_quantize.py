@@ -123,3 +123,36 @@ def test_dequantize_matches_oracle_large(g):
     out = int4_hip.dequantize_int4(qw, s, z, torch.bfloat16).cpu()
     ref = O.f32_to_bf16_bits(O.dequantize_int4(qw.cpu().numpy(), bits_of(s), bits_of(z), "bf16"))
     np.testing.assert_array_equal(bits_of(out), ref)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("g", [32, 128])
+def test_quantize_rounding_boundaries(dt, g):
+    """Weights at and a few ulps around (k + 1/2) * scale, where
+    floor(w / scale + 0.5) changes value: the kernel's reciprocal path must
+    defer to the exact division on every one of them."""
+    N, K = 256, 1024
+    rng = np.random.default_rng(11 + g)
+    tdt = TDT[dt]
+    ngroups = K // g
+    # scales m * 2^e (m odd, <= 7) keep 15 * scale and every (k + 1/2) * scale
+    # exactly representable in bf16 and fp16, so exact ties occur
+    m = rng.choice([1.0, 3.0, 5.0, 7.0], (N, ngroups))
+    e = rng.integers(-12, -7, (N, ngroups)).astype(np.float64)
+    scale = torch.from_numpy((m * 2.0 ** e).astype(np.float32))
+    k = torch.from_numpy(rng.integers(-5, 9, (N, K)).astype(np.float32))
+    w = ((k + 0.5) * scale.repeat_interleave(g, dim=1)).to(tdt)
+    # nudge by -2..2 ulps of the weight dtype
+    bits = w.view(torch.int16).to(torch.int32)
+    bits = bits + torch.from_numpy(rng.integers(-2, 3, (N, K)).astype(np.int32))
+    w = bits.to(torch.int16).view(tdt)
+    # pin each group's range to [-5, 10] * scale: the scale is the chosen one
+    # and the zero point 5
+    w[:, 0::g] = (-5.0 * scale).to(tdt)
+    w[:, 1::g] = (10.0 * scale).to(tdt)
+    print(f"[quantize boundaries] G={g} {dt}", flush=True)
+    qw, s, z = _quantize_np(w.to(DEV), g)
+    rq, rs, rz = O.quantize_int4(bits_of(w), dt, g)
+    np.testing.assert_array_equal(qw, rq)
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(z, rz)
