@@ -382,7 +382,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 // pf3_kernel: pf2's tiling with a deeper pipeline (K a multiple of 64).
 //
 //  * Activation tiles go straight from memory to LDS (128-bit direct-to-LDS
-//    buffer loads: lane l of a load lands at base + 16 l), three K steps in a
+//    buffer loads: lane l of a load lands at base + 16 l), four K steps in a
 //    ring, so they need no staging registers.  LDS chunk (row, c) of 16 bytes
 //    sits at position row * 8 + (c ^ ((row >> 1) & 7)): the 16 lanes that a
 //    128-bit LDS read serves together (16 consecutive rows, one chunk each)
@@ -392,9 +392,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 //  * Loads run two K steps ahead.  Every step issues the same number of
 //    loads, so "this wave's activations of step t have landed" is one fixed
 //    s_waitcnt vmcnt(N); a raw s_barrier then makes all waves' chunks
-//    visible (and frees the slot of step t - 1 for step t + 2).  The barrier
-//    is written without a memory fence because the fence would wait for every
-//    outstanding load, including the prefetched ones.
+//    visible.  The barrier is written without a memory fence because the
+//    fence would wait for every outstanding load, including the prefetched
+//    ones.
+//  * Software pipeline over the four 16-deep K sub-steps of a step: while
+//    the MFMAs of sub-step j run, the wave reads the A fragments of j + 1
+//    from LDS and dequantizes the B fragments of j + 1.  The barrier for
+//    step t + 1 sits between sub-steps 2 and 3 of step t, so sub-step 3
+//    already prefetches step t + 1's first fragments.  Passing that barrier
+//    means every wave is done with step t - 1, whose LDS slot ((t + 3) % 4)
+//    and register set ((t + 3) % 3, last dequantized during sub-step 2) are
+//    then refilled for step t + 3.
 // 16 bytes per lane from a raw buffer straight into LDS at lds + 16 * lane.
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
@@ -408,8 +416,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   constexpr int LPS = XL + 2 * NSZ + 4;  // loads per step and wave
   constexpr int WAITN = 2 * NSZ + 4 + LPS;  // loads issued after a step's activation loads
   constexpr int WAIT_IMM = (WAITN & 15) | 0x70 | 0xF00 | ((WAITN >> 4) << 14);
+  constexpr int SLOT = PF2_BM * PF2_BK;  // elements of one LDS slot
   static_assert(WAITN < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(16))) uint16_t xs[3][PF2_BM * PF2_BK];
+  __shared__ __attribute__((aligned(16))) uint16_t xs[4 * SLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -464,7 +473,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   auto issue = [&](Regs& r, int st) {  // step st (0-based within this split)
     const uint32_t lmask = st < nsteps ? 0u : OOB;  // scalar
     const int kt = kt0 + st;
-    uint16_t* slot = xs[st % 3];
+    uint16_t* slot = xs + (st & 3) * SLOT;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < XL; ++j)
@@ -491,29 +500,41 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
-  auto compute = [&](const Regs& r, int st) {
-    const uint16_t* xb = xs[st % 3];
-    GroupConst gc[2];
+  // pipeline registers: A and B fragments of the sub-step being multiplied
+  // and of the next one; the group constants of the step being dequantized
+  F af[2][4], bf[2][2];
+  GroupConst gc[2];
+  auto load_a = [&](int st, int ks, F* out) {
+    const uint16_t* xb = xs + (st & 3) * SLOT;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      if (ks == 0 || SZK) {
-        const int j = SZK ? ks : 0;
+    for (int mb = 0; mb < 4; ++mb) out[mb] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(&xb[a_off[mb][ks]]));
+  };
+  auto dequant_b = [&](const Regs& r, int ks, F* out) {
+    if (ks == 0 || SZK) {
+      const int j = SZK ? ks : 0;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          gc[nb] = make_group_const((uint16_t)(r.s[j] >> (16 * nb)), (uint16_t)(r.z[j] >> (16 * nb)));
-      }
-      F af[4], bf[2];
+      for (int nb = 0; nb < 2; ++nb)
+        gc[nb] = make_group_const((uint16_t)(r.s[j] >> (16 * nb)), (uint16_t)(r.z[j] >> (16 * nb)));
+    }
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) af[mb] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(&xb[a_off[mb][ks]]));
+    for (int nb = 0; nb < 2; ++nb) out[nb] = dequant_word<DT>(r.w[ks][nb], gc[nb], magic);
+  };
+  auto mfma = [&](const F* af_, const F* bf_) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) bf[nb] = dequant_word<DT>(r.w[ks][nb], gc[nb], magic);
+    for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+      for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Mfma<DT>::m32(af_[mb], bf_[nb], acc[mb][nb]);
+  };
+  // one MFMA, then (for the first four) one LDS read, then a few VALU
+  auto interleave = [&]() {
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Mfma<DT>::m32(af[mb], bf[nb], acc[mb][nb]);
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
     }
   };
-  // wait for this wave's activation loads of step st, then for every wave
+  // wait for this wave's activation loads of the next step, then for every wave
   auto sync_step = [&]() {
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(WAIT_IMM);
@@ -521,21 +542,46 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
+  // step st from register set cur; nxt holds step st + 1, and cur is
+  // refilled with step st + 3 once the barrier is passed
+  auto step = [&](Regs& cur, const Regs& nxt, int st) {
+#pragma unroll
+    for (int ks = 0; ks < 3; ++ks) {
+      const int c = ks & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      load_a(st, ks + 1, af[c ^ 1]);
+      dequant_b(cur, ks + 1, bf[c ^ 1]);
+      mfma(af[c], bf[c]);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    sync_step();
+    issue(cur, st + 3);
+    load_a(st + 1, 0, af[0]);
+    dequant_b(nxt, 0, bf[0]);
+    mfma(af[1], bf[1]);
+    interleave();
+    __builtin_amdgcn_sched_barrier(0);
+  };
 
   Regs r0, r1, r2;
   issue(r0, 0);
   issue(r1, 1);
-  for (int st = 0; st < nsteps; st += 3) {
-    sync_step();
-    issue(r2, st + 2);
-    compute(r0, st);
-    sync_step();
-    issue(r0, st + 3);
-    if (st + 1 < nsteps) compute(r1, st + 1);
-    sync_step();
-    issue(r1, st + 4);
-    if (st + 2 < nsteps) compute(r2, st + 2);
+  sync_step();
+  issue(r2, 2);
+  load_a(0, 0, af[0]);
+  dequant_b(r0, 0, bf[0]);
+  // whole register-set rotations in the loop, so that every path into its
+  // head has issued the same loads in the same order (the compiler's vmcnt
+  // bookkeeping then stays exact); the one or two remaining steps after it
+  int st = 0;
+  for (; st + 3 <= nsteps; st += 3) {
+    step(r0, r1, st);
+    step(r1, r2, st + 1);
+    step(r2, r0, st + 2);
   }
+  if (st < nsteps) step(r0, r1, st);
+  if (st + 1 < nsteps) step(r1, r2, st + 1);
   __builtin_amdgcn_s_waitcnt(0);  // no load (and no LDS write) outstanding past the loop
 
   const int n = n0w + 2 * l32;
