@@ -211,7 +211,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-passes", type=int, default=30)
     ap.add_argument("--only", default="all",
-                    help="comma list of sections to run: decode, perlinear, splitk, prefill, quantize "
+                    help="comma list of sections to run: decode, perlinear, splitk, prefill, quantize, llama "
                          "(profiling runs use one section; the JSON line needs 'decode')")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 32 MiB device copy (for scaling FETCH_SIZE/WRITE_SIZE counters)")
@@ -221,7 +221,8 @@ def main() -> int:
     if args.summarize_prof:
         print(summarize_prof(Path(args.summarize_prof)))
         return 0
-    only = set(args.only.split(",")) if args.only != "all" else {"decode", "perlinear", "splitk", "prefill", "quantize"}
+    only = set(args.only.split(",")) if args.only != "all" else {"decode", "perlinear", "splitk", "prefill", "quantize",
+                                                                  "llama"}
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the W4A16 path has no collective); "
               "run with --gpus 1", file=sys.stderr)
@@ -369,6 +370,18 @@ def main() -> int:
             del xsM
     torch.cuda.synchronize()
 
+    # ---------------------------- end to end: random-init Llama-3.2-1B with Int4Linear
+    llama = None
+    if "llama" in only:
+        from int4_hip.llama import run_eval
+        log("llama: 512-token prefill + 128 graph decode steps, bf16 then W4 ...")
+        try:
+            llama = run_eval(prompt_len=512, new_tokens=128, group_size=G)
+            llama.pop("config", None)
+        except Exception as e:  # reported in the line; the kernel figures above stand
+            llama = {"error": repr(e)[:400]}
+        torch.cuda.synchronize()
+
     # ------------------------------------------------- CPU baseline (rank 0, N=1)
     cpu = None
     if not args.no_cpu:
@@ -415,6 +428,7 @@ def main() -> int:
         "prefill_m2048_mfma_frac": round(pre[2048]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4) if pre else None,
         "quantize_us_per_block": round(q_ms * 1e3, 2) if q_ms else None,
         "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None,
+        "llama_1b_w4": llama,
         "device": torch.cuda.get_device_name(dev),
     }
     print(json.dumps(out), flush=True)

@@ -668,20 +668,45 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
   }
   const int G = problems[0].group_size;
+  // M == 1 tile width: about 128 KB of packed weights per workgroup (128
+  // columns up to K = 2048, 64 up to 4096 or for group 32, else 32); each
+  // narrowing level halves it where a tiling exists (128 -> 64 -> 32, the 32
+  // column tiling needs groups >= 64).  A launch narrows while the narrower
+  // grid still fits one workgroup per CU, so a lone small linear spreads over
+  // the chip instead of a few CUs; a decoder block's 7 linears stay at level 0.
+  auto one_width = [&](int64_t K, int level) {
+    int tn = K <= 2048 ? 128 : (K <= 4096 || G < 64) ? 64 : 32;
+    for (int l = 0; l < level; ++l) {
+      if (tn == 128)
+        tn = 64;
+      else if (tn == 64 && G >= 64 && K <= 8192)
+        tn = 32;
+    }
+    return tn;
+  };
+  int level = 0;
+  if (cu_tiles) {
+    const int cus = device_cu_count();
+    while (level < 2) {
+      int64_t next = 0;
+      for (int i = 0; i < count; ++i) {
+        const int tn = one_width(problems[i].K, level + 1);
+        next += (problems[i].N + tn - 1) / tn;
+      }
+      if (next > cus) break;
+      ++level;
+    }
+  }
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     int vec = 1, cfg = 0, tn = 16;
     if (cu_tiles) {
-      // about 128 KB of packed weights per workgroup
       vec = 4;
-      if (q.K <= 2048) {
-        tn = 128, cfg = w4::kCfgT128;
-      } else if (q.K <= 4096 || G < 64) {
-        tn = 64, cfg = q.K <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring;
-      } else {
-        tn = 32, cfg = q.K <= 8192 ? w4::kCfgT32 : w4::kCfgT32Ring;
-      }
+      tn = one_width(q.K, level);
+      cfg = tn == 128 ? w4::kCfgT128
+          : tn == 64  ? (q.K <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring)
+                      : (q.K <= 8192 ? w4::kCfgT32 : w4::kCfgT32Ring);
     } else if (q.N % 4 == 0 && qa % 16 == 0 && sa % 8 == 0 && za % 8 == 0 && q.K <= 4096) {
       vec = 4, tn = 64;
     } else if (q.N % 2 == 0 && qa % 8 == 0 && sa % 4 == 0 && za % 4 == 0) {
