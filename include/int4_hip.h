@@ -98,10 +98,12 @@ size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
  * accumulation, y in x's dtype.  x: bf16/fp16, any strides (stride_xm,
  * stride_xk).  qweight/scales/zeros dense row-major as above.  y: row stride
  * ldy (>= N), unit column stride.  Launch regimes (same boundaries as the
- * reference): M == 1 decode GEMV in one launch (long K split over workgroups,
- * finished by the last one in split order); 2 <= M <= 64 split-K with fp32
- * partials in `workspace` and a fixed-order reduce kernel; M > 64 tiled MFMA
- * GEMM.  Every regime is bit-identical run to run.
+ * reference): M <= 16 (group sizes >= 32) the factored decode kernel in one
+ * launch, no workspace; 17 <= M <= 64 (and group sizes < 32) split-K with
+ * fp32 partials in `workspace` and a fixed-order reduce kernel; M > 64 tiled
+ * MFMA GEMM, itself split over K with the same partials-and-reduce scheme
+ * when the shape leaves too few tiles to fill the chip.  Every regime is
+ * bit-identical run to run.
  * Replaces: int4_triton/gemm.py:303-309 (w4a16_matmul) and its dispatcher
  * _matmul, :234-300 (kernels :74-157, :171-182, :185-220).
  */
