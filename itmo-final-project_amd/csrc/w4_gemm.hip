@@ -22,6 +22,9 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
                       void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
 size_t w4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int w4_prefill_fast_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
+                           int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
+                           void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
 
 // Reference regime boundary: M <= SMALL_M = 64 uses split-K (gemm.py:17, 265).
 static constexpr int64_t kSmallM = 64;
@@ -39,9 +42,13 @@ extern "C" size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int gro
   } else if (M <= kDecodeM) {
     scratch = w4_gemv_workspace_bytes(M, N, K, group_size);
   } else {
+    // the pipelined MFMA kernel or, for strided / unaligned / K % 64 != 0
+    // operands, the skinny kernel: room for either
     const size_t a = w4_skinny_workspace_bytes(M, N, K, (N % 4) == 0);
     const size_t b = w4_skinny_workspace_bytes(M, N, K, false);
+    const size_t c = w4_prefill_workspace_bytes(M, N, K);
     scratch = a > b ? a : b;
+    scratch = scratch > c ? scratch : c;
   }
   return scratch > 0 ? W4_WORKSPACE_COUNTER_BYTES + scratch : 0;
 }
@@ -85,9 +92,13 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
   if (M <= kDecodeM)
     return w4_gemv_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
                           counters, scratch, scratch_bytes, st);
-  if (M <= kSmallM)
+  if (M <= kSmallM) {
+    const int rc = w4_prefill_fast_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros,
+                                          (int)G, y, ldy, scratch, scratch_bytes, st);
+    if (rc != W4_ERR_UNSUPPORTED) return rc;
     return w4_skinny_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y,
                             ldy, scratch, scratch_bytes, st);
+  }
   return w4_prefill_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
                            scratch, scratch_bytes, st);
 }

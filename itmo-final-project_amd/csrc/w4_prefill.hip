@@ -408,15 +408,17 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
 }
 
-template <int DT, int NW, bool SZK>
+template <int DT, int NW, bool SZK, int MB>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_kernel(Pf2Args a) {
   typedef typename Act<DT>::frag F;
-  constexpr int XL = 16 / NW;        // direct-to-LDS activation loads per wave per step (1 KB each)
+  constexpr int BM = 32 * MB;        // rows per tile: MB blocks of 32
+  constexpr int XL = BM / 8 / NW;    // direct-to-LDS activation loads per wave per step (1 KB each)
+  static_assert(XL >= 1, "activation loads per wave");
   constexpr int NSZ = SZK ? 4 : 1;   // scale (and zero) loads per step
   constexpr int LPS = XL + 2 * NSZ + 4;  // loads per step and wave
   constexpr int WAITN = 2 * NSZ + 4 + LPS;  // loads issued after a step's activation loads
   constexpr int WAIT_IMM = (WAITN & 15) | 0x70 | 0xF00 | ((WAITN >> 4) << 14);
-  constexpr int SLOT = PF2_BM * PF2_BK;  // elements of one LDS slot
+  constexpr int SLOT = BM * PF2_BK;  // elements of one LDS slot
   static_assert(WAITN < 64, "vmcnt range");
   __shared__ __attribute__((aligned(16))) uint16_t xs[4 * SLOT];
 
@@ -429,7 +431,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int tmn = t - split * a.tiles_mn;
   const int tile_m = tmn / a.tiles_n;
   const int tile_n = tmn - tile_m * a.tiles_n;
-  const int m0 = tile_m * PF2_BM;
+  const int m0 = tile_m * BM;
   const int n0w = (tile_n * NW + wn) * 64;
   const int N = a.N;
   const int KT = a.K / PF2_BK;
@@ -455,16 +457,15 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const uint32_t w_lane = ((uint32_t)lh * (uint32_t)N + (uint32_t)(n0w + 2 * l32)) * 4u;
   const uint32_t sz_col = (uint32_t)(n0w + 2 * l32) * 2u;
   const uint32_t magic = fp16_magic_vgpr();
-  // A-fragment read offsets (elements) for mb = 0, ks = 0: row l32, chunk lh
-  int a_off[4][4];
+  // A-fragment read offsets (elements) of block mb = 0: row l32, chunk 2 ks + lh.
+  // Block mb adds 32 rows (2048 elements, an immediate offset): its rows have
+  // the same swizzle since (mb * 32 + l32) >> 1 & 7 == (l32 >> 1) & 7.
+  int a_off[4];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int row = mb * 32 + l32;
-      const int c = ks * 2 + lh;
-      a_off[mb][ks] = (row * 8 + (c ^ ((row >> 1) & 7))) * 8;
-    }
+  for (int ks = 0; ks < 4; ++ks) {
+    const int c = ks * 2 + lh;
+    a_off[ks] = (l32 * 8 + (c ^ ((l32 >> 1) & 7))) * 8;
+  }
 
   struct Regs {
     u32x2 w[4];
@@ -492,9 +493,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[MB][2];
 #pragma unroll
-  for (int mb = 0; mb < 4; ++mb)
+  for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
@@ -502,12 +503,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 
   // pipeline registers: A and B fragments of the sub-step being multiplied
   // and of the next one; the group constants of the step being dequantized
-  F af[2][4], bf[2][2];
+  F af[2][MB], bf[2][2];
   GroupConst gc[2];
   auto load_a = [&](int st, int ks, F* out) {
     const uint16_t* xb = xs + (st & 3) * SLOT;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) out[mb] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(&xb[a_off[mb][ks]]));
+    for (int mb = 0; mb < MB; ++mb)
+      out[mb] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(&xb[a_off[ks] + mb * 2048]));
   };
   auto dequant_b = [&](const Regs& r, int ks, F* out) {
     if (ks == 0 || SZK) {
@@ -521,17 +523,17 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   };
   auto mfma = [&](const F* af_, const F* bf_) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Mfma<DT>::m32(af_[mb], bf_[nb], acc[mb][nb]);
   };
-  // one MFMA, then (for the first four) one LDS read, then a few VALU
+  // one MFMA, then (for the first MB) one LDS read, then a few VALU
   auto interleave = [&]() {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 2 * MB; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i < 4) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      if (i < MB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 24 / MB, 0);
     }
   };
   // wait for this wave's activation loads of the next step, then for every wave
@@ -587,7 +589,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int n = n0w + 2 * l32;
   if (n < N) {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + mb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
@@ -613,39 +615,56 @@ using namespace w4host;
 namespace {
 
 struct Pf2Plan {
-  int nw = 0, splits = 1, kt_per_split = 0, tiles_n = 0, tiles_mn = 0;
+  int nw = 0, mb = 4, splits = 1, kt_per_split = 0, tiles_n = 0, tiles_mn = 0;
   size_t ws = 0;
 };
 
 // Static launch table (pure function of the shape and the CU count).  Cost
-// model: MFMA work spread over min(waves, 4 * CUs) SIMDs, plus the fp32
-// partials written and re-read at HBM speed and one more launch when split.
+// model, fitted to MI355X timings of pf3 on the Llama shapes (M = 32..2048):
+// a wave alone on its SIMD needs STEP[mb] per K step of 64 (1.07 / 0.74 /
+// 0.49 us for 128 / 64 / 32-row tiles); SIMDs holding k > 1 waves run them
+// at 0.9 k STEP; four-wave workgroups on fewer workgroups than CUs lose 7 %
+// (two-wave ones spread over more CUs); every launch costs about 3 us of
+// prologue and epilogue latency plus its output bytes at 5 TB/s; split-K
+// writes fp32 partials instead and adds the reduce kernel (2.2 us plus the
+// partials read at 8 TB/s).
 Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K) {
   const int cus = device_cu_count();
   const int64_t KT = (K + w4::PF2_BK - 1) / w4::PF2_BK;
-  const int64_t tm = (M + w4::PF2_BM - 1) / w4::PF2_BM;
-  const double flops = 2.0 * (double)M * (double)N * (double)K;
-  const double simd_rate = 1024.0 * 2.4e9 * 0.6;  // flop/s of one SIMD at a sustained 60 %
   Pf2Plan best;
   double best_t = 1e30;
-  for (int nw : {4, 2}) {
-    const int64_t tn = (N + 64 * nw - 1) / (64 * nw);
-    for (int s : {1, 2, 4, 8}) {
-      const int64_t T = (KT + s - 1) / s;
-      const int64_t S = (KT + T - 1) / T;
-      if (S != s || (s > 1 && T < 4)) continue;
-      const double waves = (double)(tm * tn * S * nw);
-      const double simds = std::min(waves, 4.0 * cus);
-      double t = flops / (simds * simd_rate);
-      if (S > 1) t += 2.0 * (double)S * M * N * 4 / 5e12 + 2e-6;
-      if (t < best_t * 0.97) {
-        best_t = t;
-        best.nw = nw;
-        best.splits = (int)S;
-        best.kt_per_split = (int)T;
-        best.tiles_n = (int)tn;
-        best.tiles_mn = (int)(tm * tn);
-        best.ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+  for (int mb : {4, 2, 1}) {
+    if (mb != 4 && K % w4::PF2_BK != 0) continue;  // the register-staged kernel has 128-row tiles only
+    const double step = mb == 4 ? 1.07e-6 : mb == 2 ? 0.74e-6 : 0.49e-6;
+    const int64_t bm = 32 * mb;
+    const int64_t tm = (M + bm - 1) / bm;
+    for (int nw : {4, 2}) {
+      const int64_t tn = (N + 64 * nw - 1) / (64 * nw);
+      for (int s : {1, 2, 4, 8}) {
+        const int64_t T = (KT + s - 1) / s;
+        const int64_t S = (KT + T - 1) / T;
+        if (S != s || (s > 1 && T < 4)) continue;
+        const int64_t wgs = tm * tn * S;
+        const double per_simd = (double)(wgs * nw) / (4.0 * cus);
+        double t = (double)T * step * (per_simd <= 1.0 ? 1.0 : 0.9 * per_simd);
+        if (nw == 4 && wgs < cus) t *= 1.07;
+        t += 3e-6;
+        if (S > 1) {
+          const double part = (double)S * M * N * 4;
+          t += part / 5e12 + 2.2e-6 + part / 8e12;
+        } else {
+          t += (double)M * N * 2 / 5e12;
+        }
+        if (t < best_t * 0.97) {
+          best_t = t;
+          best.nw = nw;
+          best.mb = mb;
+          best.splits = (int)S;
+          best.kt_per_split = (int)T;
+          best.tiles_n = (int)tn;
+          best.tiles_mn = (int)(tm * tn);
+          best.ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+        }
       }
     }
   }
@@ -659,14 +678,25 @@ bool pf2_ok(const void* x, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t
          M < (1LL << 30) && ((M - 1) * sxm + K) * 2 < (1LL << 31) && (K / 8) * N * 4 < (1LL << 31);
 }
 
+template <int DT, int NW, int MB>
+void pf3_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t st) {
+  const dim3 grid((unsigned)(p.tiles_mn * p.splits)), block(NW * 64);
+  if (szk)
+    hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, true, MB>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, false, MB>), grid, block, 0, st, a);
+}
+
 template <int DT, int NW>
 void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t st) {
   const dim3 grid((unsigned)(p.tiles_mn * p.splits)), block(NW * 64);
   if (a.K % w4::PF2_BK == 0) {  // deep pipeline: whole K steps only
-    if (szk)
-      hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, true>), grid, block, 0, st, a);
+    if (p.mb == 4)
+      pf3_launch_g<DT, NW, 4>(p, szk, a, st);
+    else if (p.mb == 2)
+      pf3_launch_g<DT, NW, 2>(p, szk, a, st);
     else
-      hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, false>), grid, block, 0, st, a);
+      pf3_launch_g<DT, NW, 1>(p, szk, a, st);
   } else if (szk) {
     hipLaunchKernelGGL((w4::pf2_kernel<DT, NW, true>), grid, block, 0, st, a);
   } else {
@@ -681,6 +711,21 @@ int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_
 
 // Scratch bytes (past the workspace's counter area) of a prefill launch.
 size_t w4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K) { return plan_pf2(M, N, K).ws; }
+
+int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
+                      int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
+                      void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
+
+// The pipelined MFMA kernel for 17 <= M <= 64 as well: returns
+// W4_ERR_UNSUPPORTED (nothing launched, no message) when the activations are
+// not dense 16-byte-aligned rows or K is not a multiple of 64; the caller then
+// takes the split-K skinny kernel.
+int w4_prefill_fast_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
+                           int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
+                           void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st) {
+  if (K % w4::PF2_BK != 0 || !pf2_ok(x, M, N, K, sxm, sxk, qw, sc, ze, y, ldy)) return W4_ERR_UNSUPPORTED;
+  return w4_prefill_launch(x, x_dtype, M, N, K, sxm, sxk, qw, sc, ze, G, y, ldy, ws, ws_bytes, st);
+}
 
 int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
