@@ -217,6 +217,7 @@ struct Pf2Args {
   uint32_t x_bytes, qw_bytes, sz_bytes;
   int M, N, K, gshift;
   int tiles_n, tiles_mn, kt_per_split;
+  int y16;  // pf3: y rows 16-byte aligned and N % 8 == 0 (LDS-staged 16-byte output stores)
 };
 
 constexpr int PF2_BM = 128;
@@ -586,6 +587,36 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   if (st + 1 < nsteps) step(r1, r2, st + 1);
   __builtin_amdgcn_s_waitcnt(0);  // no load (and no LDS write) outstanding past the loop
 
+  constexpr int TW = 64 * NW;  // tile width (elements)
+  if (BM * TW <= 4 * SLOT && a.ws == nullptr && a.y16) {
+    // Output through LDS: the tile (BM x 64 NW values of the output dtype,
+    // when it fits the four ring slots) is assembled there, then written back
+    // as 16-byte chunks, whole 64 NW-wide row segments per 64 NW / 8 lanes
+    // instead of 128-byte pieces per lane pair.
+    __syncthreads();  // every wave is past its last A-fragment read
+    uint32_t* T = reinterpret_cast<uint32_t*>(xs);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = mb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        T[row * (TW / 2) + wn * 32 + l32] = (uint32_t)float_to_act_bits<DT>(acc[mb][0][r]) |
+                                            ((uint32_t)float_to_act_bits<DT>(acc[mb][1][r]) << 16);
+      }
+    __syncthreads();
+    constexpr int CPR = TW / 8;  // 16-byte chunks per tile row
+    const int n0 = tile_n * TW;
+#pragma unroll 4
+    for (int c = tid; c < BM * CPR; c += NW * 64) {
+      const int row = c / CPR, cc = c - row * CPR;
+      const int m = m0 + row, n = n0 + cc * 8;
+      if (m < a.M && n < N)
+        *reinterpret_cast<u32x4*>(a.y + (int64_t)m * a.ldy + n) =
+            *reinterpret_cast<const u32x4*>(&T[row * (TW / 2) + cc * 4]);
+    }
+    return;
+  }
+
   const int n = n0w + 2 * l32;
   if (n < N) {
 #pragma unroll
@@ -754,6 +785,7 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
     a.tiles_n = p.tiles_n;
     a.tiles_mn = p.tiles_mn;
     a.kt_per_split = p.kt_per_split;
+    a.y16 = (N % 8 == 0 && ldy % 8 == 0 && (uintptr_t)y % 16 == 0) ? 1 : 0;
     const bool szk = G < 64;
     if (x_dtype == W4_DTYPE_BF16) {
       if (p.nw == 4)
