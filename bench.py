@@ -378,6 +378,11 @@ def main() -> int:
         try:
             llama = run_eval(prompt_len=512, new_tokens=128, group_size=G)
             llama.pop("config", None)
+            # the reference's --quantize-lm-head variant (untied, 128256 x 2048 lm_head in int4)
+            lm = run_eval(prompt_len=512, new_tokens=128, group_size=G, quantize_lm_head=True, reps=2)
+            llama["quantize_lm_head"] = {k: lm[k] for k in (
+                "linear_weight_bytes", "model_bytes", "w4_prefill_tokens_per_s", "w4_decode_tokens_per_s",
+                "w4_decode_ms_per_token", "vs_fake_prefill_top1_agreement", "vs_fake_prefill_kl_mean")}
         except Exception as e:  # reported in the line; the kernel figures above stand
             llama = {"error": repr(e)[:400]}
         torch.cuda.synchronize()

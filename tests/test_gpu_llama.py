@@ -59,9 +59,10 @@ def test_graph_decode_matches_eager():
     assert torch.equal(torch.cat(got), torch.cat(want))
 
 
-def test_run_eval_small():
-    print("[llama] run_eval small", flush=True)
-    r = run_eval(prompt_len=48, new_tokens=8, cfg=SMALL, reps=1)
+@pytest.mark.parametrize("lm_head", [False, True])
+def test_run_eval_small(lm_head):
+    print(f"[llama] run_eval small lm_head={lm_head}", flush=True)
+    r = run_eval(prompt_len=48, new_tokens=8, cfg=SMALL, reps=1, quantize_lm_head=lm_head)
     assert r["linear_weight_bytes"] < r["linear_weight_bytes_before"] / 3
     for k in ("bf16_prefill_tokens_per_s", "w4_prefill_tokens_per_s", "bf16_decode_tokens_per_s",
               "w4_decode_tokens_per_s", "prefill_top1_agreement", "prefill_kl_mean"):
