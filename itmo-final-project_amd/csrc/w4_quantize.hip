@@ -117,25 +117,36 @@ __device__ __forceinline__ void load8(const uint16_t* __restrict__ w, int64_t n,
   }
 }
 
-constexpr int QROWS = 64;  // columns n per wave tile (= lanes, for the stores)
-constexpr int QWAVES = 4;  // independent wave tiles per workgroup
+constexpr int QROWS = 64;  // columns n per tile (= lanes, for the stores)
+constexpr int QWAVES = 4;  // waves per workgroup (two-pass kernel)
+constexpr int QSWAVES = 8;  // waves per workgroup (single-pass kernel)
+
+// Waves sharing one (group, 64-column) tile: 64 rows split between up to eight
+// waves, each taking whole iterations of 512 / G rows (a lone wave per tile
+// runs one long dependent chain per SIMD and leaves most of the chip idle).
+constexpr int quantize_waves_per_tile(int G) { return G / 8 < QSWAVES ? G / 8 : QSWAVES; }
 
 // Single-pass kernel for G <= 512: lanes_per_row = G/8 lanes each own one
 // packed word of a row; 64/lanes_per_row rows are processed per iteration.
 template <int DT, int G, bool VEC>
-__global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
+__global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
     const uint16_t* __restrict__ w, int64_t N, int64_t K, int64_t swn, int64_t swk,
     int32_t* __restrict__ qw, uint16_t* __restrict__ sc, uint16_t* __restrict__ ze,
     int64_t tiles_n, int64_t tiles_total) {
-  constexpr int L = G / 8;            // lanes per row (4..64)
+  constexpr int L = G / 8;            // lanes per row (1..64)
   constexpr int RPI = 64 / L;         // rows per iteration
-  __shared__ uint32_t tile[QWAVES][L][QROWS + 1];
-  __shared__ uint16_t st_s[QWAVES][QROWS];
-  __shared__ uint16_t st_z[QWAVES][QROWS];
+  constexpr int WPT = quantize_waves_per_tile(G);
+  constexpr int TPB = QSWAVES / WPT;  // tiles per workgroup
+  constexpr int RW = QROWS / WPT;     // rows per wave
+  static_assert(RW % RPI == 0 && L % WPT == 0, "wave split of a tile");
+  __shared__ uint32_t tile[TPB][L][QROWS + 1];
+  __shared__ uint16_t st_s[TPB][QROWS];
+  __shared__ uint16_t st_z[TPB][QROWS];
 
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * QWAVES + wv;
+  const int ts = wv / WPT, sub = wv % WPT;  // tile slot, row slice of this wave
+  const int64_t t = (int64_t)blockIdx.x * TPB + ts;
   const bool active = t < tiles_total;
   const int64_t g = active ? t / tiles_n : 0;
   const int64_t n0 = active ? (t % tiles_n) * QROWS : 0;
@@ -144,7 +155,7 @@ __global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
 
   // Rows are loaded in batches of up to 16 per lane before any is used, so a
   // wave keeps 16 row segments in flight instead of one.
-  constexpr int IT = QROWS / RPI;
+  constexpr int IT = RW / RPI;
   constexpr int B = IT < 16 ? IT : 16;
   const uint32_t w_bytes = VEC ? (uint32_t)(((N - 1) * swn + K) * 2) : 0u;
   const __amdgpu_buffer_rsrc_t rw =
@@ -154,7 +165,7 @@ __global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
       u32x4 raw[B];
 #pragma unroll
       for (int i = 0; i < B; ++i) {
-        const int row = (b0 + i) * RPI + rsub;
+        const int row = sub * RW + (b0 + i) * RPI + rsub;
         const int64_t n = n0 + row;
         if constexpr (VEC) {
           // rows past N read zeros (buffer range check)
@@ -184,7 +195,7 @@ __global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
       if (__builtin_amdgcn_ballot_w64(has_nan) == 0) {
 #pragma unroll
         for (int i = 0; i < B; ++i) {
-          const int row = (b0 + i) * RPI + rsub;
+          const int row = sub * RW + (b0 + i) * RPI + rsub;
           float v[8];
           unpack_row8<DT>(raw[i], v);
           float mx = v[0], mn = v[0];
@@ -205,16 +216,16 @@ __global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
           // make it 0: both take the exact path
           if (!(st.scale > 0.0f && st.scale < __builtin_inff())) flag = 1;
           if (flag != 0) word = quantize_pack8(v, st);
-          tile[wv][seg][row] = word;
+          tile[ts][seg][row] = word;
           if (seg == 0) {
-            st_s[wv][row] = scale_bits(st.scale);
-            st_z[wv][row] = zero_bits(st.zero);
+            st_s[ts][row] = scale_bits(st.scale);
+            st_z[ts][row] = zero_bits(st.zero);
           }
         }
       } else {
 #pragma unroll
         for (int i = 0; i < B; ++i) {
-          const int row = (b0 + i) * RPI + rsub;
+          const int row = sub * RW + (b0 + i) * RPI + rsub;
           float v[8];
           unpack_row8<DT>(raw[i], v);
           float mx = v[0], mn = v[0];
@@ -229,10 +240,10 @@ __global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
             mn = min_nan(mn, __shfl_xor(mn, off, 64));
           }
           const QStats st = group_stats(mx, mn);
-          tile[wv][seg][row] = quantize_pack8(v, st);
+          tile[ts][seg][row] = quantize_pack8(v, st);
           if (seg == 0) {
-            st_s[wv][row] = scale_bits(st.scale);
-            st_z[wv][row] = zero_bits(st.zero);
+            st_s[ts][row] = scale_bits(st.scale);
+            st_z[ts][row] = zero_bits(st.zero);
           }
         }
       }
@@ -244,9 +255,11 @@ __global__ __launch_bounds__(QWAVES * 64) void quantize_small_group_kernel(
     if (n < N) {
       const int64_t k8_0 = g * L;
 #pragma unroll 4
-      for (int kk = 0; kk < L; ++kk) qw[(k8_0 + kk) * N + n] = (int32_t)tile[wv][kk][lane];
-      sc[g * N + n] = st_s[wv][lane];
-      ze[g * N + n] = st_z[wv][lane];
+      for (int kk = sub; kk < L; kk += WPT) qw[(k8_0 + kk) * N + n] = (int32_t)tile[ts][kk][lane];
+      if (sub == 0) {
+        sc[g * N + n] = st_s[ts][lane];
+        ze[g * N + n] = st_z[ts][lane];
+      }
     }
   }
 }
@@ -402,8 +415,10 @@ static void launch_quantize(const uint16_t* w, int64_t N, int64_t K, int64_t swn
                             int G, int32_t* qw, uint16_t* sc, uint16_t* ze, hipStream_t st) {
   const int64_t tiles_n = (N + w4::QROWS - 1) / w4::QROWS;
   const int64_t tiles_total = tiles_n * (K / G);
-  const dim3 grid((unsigned)((tiles_total + w4::QWAVES - 1) / w4::QWAVES));
-  const dim3 block(w4::QWAVES * 64);
+  const bool small = G <= 512;
+  const int64_t tpb = small ? w4::QSWAVES / w4::quantize_waves_per_tile(G) : w4::QWAVES;
+  const dim3 grid((unsigned)((tiles_total + tpb - 1) / tpb));
+  const dim3 block((small ? w4::QSWAVES : w4::QWAVES) * 64);
 #define W4_QS(GG)                                                                         \
   case GG:                                                                                \
     hipLaunchKernelGGL((w4::quantize_small_group_kernel<DT, GG, VEC>), grid, block, 0, st, \
