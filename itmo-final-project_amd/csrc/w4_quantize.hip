@@ -55,29 +55,26 @@ __device__ __forceinline__ uint32_t quantize_pack8(const float v[8], QStats st) 
 }
 
 // Fast form of quantize_pack8 for finite weights and a finite nonzero scale
-// (group_stats' scale is then in [2^-24, 65504]).  floor(w/scale + 0.5) is
-// taken from the reciprocal product w * rcp(scale): v_rcp_f32 is within 1 ulp,
-// so |w*rcp - w/scale| <= |w/scale| * 2^-22 and, for |w/scale| < 16.0001,
-// fl(fl(w*rcp) + 0.5) lies within 6e-6 of fl(fl(w/scale) + 0.5).  Both then
-// have the same floor unless that value is within 2^-15 of an integer.
-// *exact is nonzero when some element is, or has |w*rcp| not below 16; the
-// caller then repacks the word with quantize_pack8.  Otherwise the word is
+// (group_stats' scale is then in [2^-24, 65504]).  t = w * rcp(scale) + 0.5 +
+// zero in one fma (zero is an integer in [0, 15]): v_rcp_f32 is within 1 ulp,
+// so while |w/scale| < 32, t lies within 8e-6 of the reference's
+// fl(fl(w/scale) + 0.5) + zero and both floors agree unless t is within 2^-15
+// of an integer; beyond that range both clamp to the same end (0 or 15).
+// *dev returns max |frac(t) - 1/2| over the word: above 1/2 - 2^-15 the
+// caller repacks the word with quantize_pack8.  Otherwise the word is
 // bit-identical to quantize_pack8's.
-__device__ __forceinline__ uint32_t quantize_pack8_fast(const float v[8], QStats st, float rcp, uint32_t* exact) {
-#pragma clang fp contract(off)
-  constexpr float EPS = 1.0f / 32768.0f;
-  uint32_t word = 0, flag = 0;
+__device__ __forceinline__ uint32_t quantize_pack8_fast(const float v[8], QStats st, float rcp, float* dev) {
+  const float c = 0.5f + st.zero;
+  uint32_t word = 0;
+  float m = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float r = v[i] * rcp;
-    const float t = r + 0.5f;
+    const float t = __builtin_fmaf(v[i], rcp, c);
     const float f = floorf(t);
-    const float d = t - f;
-    flag |= (uint32_t)(!(fabsf(r) < 16.0f) || d < EPS || d > 1.0f - EPS) << i;
-    const float qf = fminf(fmaxf(f + st.zero, 0.0f), 15.0f);
-    word += (uint32_t)(int)qf << (4 * i);
+    m = fmaxf(m, fabsf((t - f) - 0.5f));
+    word |= (uint32_t)__builtin_amdgcn_fmed3f(f, 0.0f, 15.0f) << (4 * i);
   }
-  *exact = flag;
+  *dev = m;
   return word;
 }
 
@@ -210,12 +207,12 @@ __global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
             mn = fminf(mn, __shfl_xor(mn, off, 64));
           }
           const QStats st = group_stats(mx, mn);
-          uint32_t flag;
-          uint32_t word = quantize_pack8_fast(v, st, __builtin_amdgcn_rcpf(st.scale), &flag);
-          // an infinite weight makes the scale infinite and fp16 rounding can
-          // make it 0: both take the exact path
-          if (!(st.scale > 0.0f && st.scale < __builtin_inff())) flag = 1;
-          if (flag != 0) word = quantize_pack8(v, st);
+          float dev;
+          uint32_t word = quantize_pack8_fast(v, st, __builtin_amdgcn_rcpf(st.scale), &dev);
+          // near a rounding boundary, or an infinite weight (infinite scale)
+          // or a scale rounded to 0 in fp16: the exact path
+          if (!(dev <= 0.5f - 1.0f / 32768.0f) || !(st.scale > 0.0f && st.scale < __builtin_inff()))
+            word = quantize_pack8(v, st);
           tile[ts][seg][row] = word;
           if (seg == 0) {
             st_s[ts][row] = scale_bits(st.scale);
