@@ -45,6 +45,11 @@ def block_bytes(M: int, g: int = G) -> int:
     return sum(N * K // 2 + 4 * N * K // g + 2 * M * K + 2 * M * N for _, N, K in LINEARS)
 
 
+def lin_bytes(N: int, K: int, M: int = 1, g: int = G) -> int:
+    """Algorithmic bytes of one linear: packed weights, scales + zeros, x, y."""
+    return N * K // 2 + 4 * N * K // g + 2 * M * K + 2 * M * N
+
+
 def block_flops(M: int) -> int:
     return sum(2 * M * N * K for _, N, K in LINEARS)
 
@@ -296,7 +301,7 @@ def main() -> int:
     def single(i, j):
         return lambda: int4_hip.w4a16_matmul(xs1[i][j], *packed[i][j])
 
-    per_lin, ms7 = {}, None
+    per_lin, ms7, resident = {}, None, None
     if "perlinear" in only:
         for j, (name, N, K) in enumerate(LINEARS):
             gj = graph_of(lambda j=j: [single(i, j)() for i in range(nsets)], stream)
@@ -307,6 +312,16 @@ def main() -> int:
         time_graph(g7, 2, stream)
         ms7 = time_graph(g7, 10, stream) / nsets
         del g7
+        # cache-resident figures (one weight set, 32 MB, replayed: it stays in
+        # the 256 MB Infinity Cache), comparable to L2-resident numbers
+        gr = graph_of(lambda: [grouped(0)() for _ in range(nsets)], stream)
+        time_graph(gr, 2, stream)
+        resident = {"grouped_us_per_block": time_graph(gr, 10, stream) / nsets * 1e3}
+        del gr
+        g7r = graph_of(lambda: [single(0, j)() for _ in range(nsets) for j in range(len(LINEARS))], stream)
+        time_graph(g7r, 2, stream)
+        resident["seven_launches_us_per_block"] = time_graph(g7r, 10, stream) / nsets * 1e3
+        del g7r
 
     # ------------------------------------------------- small-M regime
     # M in {2..64} x G in {128, 64, 32}, per-linear launches over the rotated
@@ -423,6 +438,10 @@ def main() -> int:
             "kernel_time_source": kern_ms_src},
         "cpu_baseline": cpu,
         "decode_m1_per_linear_us": {k: round(v, 3) for k, v in per_lin.items()},
+        "decode_m1_per_linear_gbps": {name: round(lin_bytes(N, K) / (per_lin[name] * 1e-6) / 1e9, 1)
+                                      for name, N, K in LINEARS if name in per_lin},
+        "decode_m1_cache_resident": None if resident is None else {
+            k: round(v, 3) for k, v in resident.items()},
         "decode_m1_7_launches_us_per_block": round(ms7 * 1e3, 3) if ms7 else None,
         "decode_m1_7_launches_gbps": round(bytes1 / (ms7 * 1e-3) / 1e9, 1) if ms7 else None,
         "small_m_7_launches": {f"G{g}": {f"M{m}": v for m, v in d.items()} for g, d in small.items()},
