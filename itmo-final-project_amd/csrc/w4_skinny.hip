@@ -281,41 +281,51 @@ __global__ __launch_bounds__(512) void skinny_kernel(SkinnyArgs a) {
 // y[m][n] = sum_{s < S} ws[s][m][n] in split order (int4_triton/gemm.py:171-182
 // is the reference's fixed-order reduce).
 // Fixed-order split-K reduce: y = sum over s = 0..S-1 of partial s, in split
-// order, cast once.  A thread owns VEC consecutive elements of the [M, N]
-// result and issues the loads of all S partials (buffer loads; splits >= S
-// take an out-of-range offset and are not added) before the first add, so the
+// order, cast once.  A thread owns U chunks of VEC consecutive elements of the
+// [M, N] result (chunk u of workgroup b: b * 256 U + 256 u + thread, so each
+// load instruction of a workgroup covers 256 consecutive chunks) and issues
+// the loads of all its chunks and splits (buffer loads; splits S..SMAX-1 take
+// an out-of-range offset and are not added) before the first add, so the
 // kernel costs one memory latency instead of S.
 constexpr int kReduceMaxSplits = 16;
-template <int DT, int VEC>
+template <int DT, int VEC, int SMAX, int U>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int S,
                                                             int64_t M, int64_t N,
                                                             uint16_t* __restrict__ y, int64_t ldy) {
   typedef typename std::conditional<VEC == 4, f32x4, float>::type V;
-  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * VEC;
   const int64_t MN = M * N;
-  if (e >= MN) return;
   const __amdgpu_buffer_rsrc_t rw =
       __builtin_amdgcn_make_buffer_rsrc((void*)ws, (short)0, (int)((uint64_t)S * MN * 4u), 0x00020000);
-  V v[kReduceMaxSplits];
+  int64_t e[U];
+  V v[U][SMAX];
 #pragma unroll
-  for (int i = 0; i < kReduceMaxSplits; ++i) {
-    const uint32_t off = i < S ? (uint32_t)(((int64_t)i * MN + e) * 4) : 0x80000000u;
-    if constexpr (VEC == 4)
-      v[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
-    else
-      v[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rw, off, 0, 0));
+  for (int u = 0; u < U; ++u) {
+    e[u] = ((int64_t)blockIdx.x * 256 * U + 256 * u + threadIdx.x) * VEC;
+    const bool in = e[u] < MN;
+#pragma unroll
+    for (int i = 0; i < SMAX; ++i) {
+      const uint32_t off = (in && i < S) ? (uint32_t)(((int64_t)i * MN + e[u]) * 4) : 0x80000000u;
+      if constexpr (VEC == 4)
+        v[u][i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
+      else
+        v[u][i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rw, off, 0, 0));
+    }
   }
-  V t = v[0];
 #pragma unroll
-  for (int i = 1; i < kReduceMaxSplits; ++i)
-    if (i < S) t += v[i];
-  const int64_t m = e / N, n = e - m * N;
-  if constexpr (VEC == 4) {
-    const uint32_t lo = (uint32_t)float_to_act_bits<DT>(t[0]) | ((uint32_t)float_to_act_bits<DT>(t[1]) << 16);
-    const uint32_t hi = (uint32_t)float_to_act_bits<DT>(t[2]) | ((uint32_t)float_to_act_bits<DT>(t[3]) << 16);
-    *reinterpret_cast<u32x2*>(y + m * ldy + n) = u32x2{lo, hi};
-  } else {
-    y[m * ldy + n] = float_to_act_bits<DT>(t);
+  for (int u = 0; u < U; ++u) {
+    if (e[u] >= MN) continue;
+    V t = v[u][0];
+#pragma unroll
+    for (int i = 1; i < SMAX; ++i)
+      if (i < S) t += v[u][i];
+    const int64_t m = e[u] / N, n = e[u] - m * N;
+    if constexpr (VEC == 4) {
+      const uint32_t lo = (uint32_t)float_to_act_bits<DT>(t[0]) | ((uint32_t)float_to_act_bits<DT>(t[1]) << 16);
+      const uint32_t hi = (uint32_t)float_to_act_bits<DT>(t[2]) | ((uint32_t)float_to_act_bits<DT>(t[3]) << 16);
+      *reinterpret_cast<u32x2*>(y + m * ldy + n) = u32x2{lo, hi};
+    } else {
+      y[m * ldy + n] = float_to_act_bits<DT>(t);
+    }
   }
 }
 
@@ -439,6 +449,28 @@ int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K
   return w4_splitk_reduce_launch(static_cast<const float*>(ws), (int)p.splits, M, N, x_dtype, y, ldy, st);
 }
 
+template <int DT, int VEC, int SMAX, int U>
+static void reduce_go(const float* ws, int S, int64_t M, int64_t N, uint16_t* y, int64_t ldy, hipStream_t st) {
+  const int64_t chunks = (M * N + VEC - 1) / VEC;
+  const dim3 grid((unsigned)((chunks + 256 * U - 1) / (256 * U)));
+  hipLaunchKernelGGL((w4::splitk_reduce_kernel<DT, VEC, SMAX, U>), grid, dim3(256), 0, st, ws, S, M, N, y, ldy);
+}
+
+// Loads per thread stay at 8-16: more elements per thread for few splits.
+template <int DT>
+static void reduce_launch_dt(bool v4, const float* ws, int S, int64_t M, int64_t N, uint16_t* y, int64_t ldy,
+                             hipStream_t st) {
+  if (!v4) {
+    if (S <= 4) reduce_go<DT, 1, 4, 4>(ws, S, M, N, y, ldy, st);
+    else reduce_go<DT, 1, 16, 1>(ws, S, M, N, y, ldy, st);
+    return;
+  }
+  if (S <= 2) reduce_go<DT, 4, 2, 4>(ws, S, M, N, y, ldy, st);
+  else if (S <= 4) reduce_go<DT, 4, 4, 2>(ws, S, M, N, y, ldy, st);
+  else if (S <= 8) reduce_go<DT, 4, 8, 1>(ws, S, M, N, y, ldy, st);
+  else reduce_go<DT, 4, 16, 1>(ws, S, M, N, y, ldy, st);
+}
+
 int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_dtype, void* y, int64_t ldy,
                             hipStream_t st) {
   const int64_t MN = M * N;
@@ -446,19 +478,10 @@ int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_
     return fail(W4_ERR_UNSUPPORTED, "w4a16_gemm: split-K reduce of %d x %lld partials unsupported", S,
                 (long long)MN);
   const bool v4 = N % 4 == 0 && ldy % 4 == 0 && (uintptr_t)y % 8 == 0;
-  const int vec = v4 ? 4 : 1;
-  const dim3 rgrid((unsigned)((MN / vec + 255) / 256));
   uint16_t* yy = static_cast<uint16_t*>(y);
-  if (x_dtype == W4_DTYPE_BF16) {
-    if (v4)
-      hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_BF16, 4>), rgrid, dim3(256), 0, st, ws, S, M, N, yy, ldy);
-    else
-      hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_BF16, 1>), rgrid, dim3(256), 0, st, ws, S, M, N, yy, ldy);
-  } else {
-    if (v4)
-      hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_FP16, 4>), rgrid, dim3(256), 0, st, ws, S, M, N, yy, ldy);
-    else
-      hipLaunchKernelGGL((w4::splitk_reduce_kernel<W4_DTYPE_FP16, 1>), rgrid, dim3(256), 0, st, ws, S, M, N, yy, ldy);
-  }
+  if (x_dtype == W4_DTYPE_BF16)
+    reduce_launch_dt<W4_DTYPE_BF16>(v4, ws, S, M, N, yy, ldy, st);
+  else
+    reduce_launch_dt<W4_DTYPE_FP16>(v4, ws, S, M, N, yy, ldy, st);
   return check_launch("w4a16_gemm (split-K reduce)");
 }
