@@ -141,12 +141,13 @@ __global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
   __shared__ uint16_t st_z[TPB][QROWS];
 
   const int lane = threadIdx.x & 63;
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: tile math stays scalar
   const int ts = wv / WPT, sub = wv % WPT;  // tile slot, row slice of this wave
-  const int64_t t = (int64_t)blockIdx.x * TPB + ts;
-  const bool active = t < tiles_total;
-  const int64_t g = active ? t / tiles_n : 0;
-  const int64_t n0 = active ? (t % tiles_n) * QROWS : 0;
+  // the host keeps tile counts below 2^31, so the tile index math is 32-bit
+  const int t = (int)blockIdx.x * TPB + ts;
+  const bool active = t < (int)tiles_total;
+  const int g = active ? t / (int)tiles_n : 0;
+  const int64_t n0 = active ? (int64_t)(t - g * (int)tiles_n) * QROWS : 0;
   const int seg = lane % L;
   const int rsub = lane / L;
 
@@ -166,7 +167,9 @@ __global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
         const int64_t n = n0 + row;
         if constexpr (VEC) {
           // rows past N read zeros (buffer range check)
-          const uint32_t off = n < N ? (uint32_t)((n * swn + g * G + seg * 8) * 2) : 0x80000000u;
+          // 32-bit offsets: the host routes only weights below 2^31 bytes here
+          const uint32_t off = n < N ? ((uint32_t)n * (uint32_t)swn + (uint32_t)(g * G + seg * 8)) * 2u
+                                     : 0x80000000u;
           raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
         } else {
           uint16_t e[8];
@@ -452,6 +455,9 @@ extern "C" int w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K, int
   if (G > (int64_t)1 << 30) return fail(W4_ERR_UNSUPPORTED, "w4_quantize: group_size too large");
   if (N == 0) return W4_OK;
   if (!w || !qweight || !scales || !zeros) return fail(W4_ERR_INVALID, "w4_quantize: null pointer");
+  if (((N + 63) / 64) * (K / G) >= (int64_t)1 << 31)
+    return fail(W4_ERR_UNSUPPORTED, "w4_quantize: %lld x %lld weight has too many tiles", (long long)N,
+                (long long)K);
   const uint16_t* wp = static_cast<const uint16_t*>(w);
   // 128-bit buffer loads: dense rows, 16-byte aligned, whole tensor within 2 GiB
   const bool vec = stride_wk == 1 && (stride_wn % 8) == 0 && ((uintptr_t)wp % 16) == 0 &&
