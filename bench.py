@@ -374,6 +374,17 @@ def main() -> int:
                 per[name] = round(time_graph(gj, 10, stream) / 4 * 1e3, 2)
                 del gj
             pre[M]["per_linear_us"] = per
+            # the same block with the projections that share an input fused
+            # (q/k/v and gate/up as grouped calls): 4 W4A16 calls instead of 7
+            gf = graph_of(lambda: [int4_hip.w4a16_matmul_grouped([xsM[0]] * 3, packed[0][0:3]),
+                                   int4_hip.w4a16_matmul(xsM[3], *packed[0][3]),
+                                   int4_hip.w4a16_matmul_grouped([xsM[4]] * 2, packed[0][4:6]),
+                                   int4_hip.w4a16_matmul(xsM[6], *packed[0][6])], stream)
+            time_graph(gf, 3, stream)
+            msf = time_graph(gf, 10, stream)
+            pre[M]["fused_qkv_gateup_us_per_block"] = round(msf * 1e3, 2)
+            pre[M]["fused_qkv_gateup_tflops"] = round(block_flops(M) / (msf * 1e-3) / 1e12, 2)
+            del gf
             w_deq = [int4_hip.dequantize_int4(*packed[0][j], torch.bfloat16) for j in range(len(LINEARS))]
             gb = graph_of(lambda: [torch.nn.functional.linear(xsM[j], w_deq[j]) for j in range(len(LINEARS))],
                           stream)

@@ -137,12 +137,19 @@ typedef struct w4a16_problem {
 size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, int64_t M);
 
 /*
- * Up to W4_MAX_GROUPED independent small-M (1 <= M <= 16) products in ONE
- * kernel launch, all with the same activation dtype and M.  Problems with a
- * long K are split over several workgroups whose fp32 partials are summed, in
- * split order, by the last workgroup of each column tile to finish; that needs
- * `workspace` (256-byte aligned, w4a16_grouped_workspace_bytes long, laid out
- * like w4a16_gemm's).  Reusing one workspace for calls that run concurrently
+ * Up to W4_MAX_GROUPED independent products, all with the same activation
+ * dtype and M; x of every problem is dense ([M, K] rows of K elements), y
+ * dense [M, N].
+ *   1 <= M <= 16: ONE kernel launch for all problems (the factored decode
+ *   kernel).  Problems with a long K may be split over several workgroups whose
+ *   fp32 partials are summed, in split order, by the last workgroup of each
+ *   column tile to finish (in `workspace`).
+ *   M > 16: problems that share one activation matrix (same x pointer, K and
+ *   group size; at most 4) run as ONE launch of the prefill kernel when its
+ *   plan for the concatenated width needs no split-K; otherwise each problem
+ *   is one w4a16_gemm call, in order, on `stream` (sharing `workspace`).
+ * `workspace`: 256-byte aligned, w4a16_grouped_workspace_bytes long, laid out
+ * like w4a16_gemm's.  Reusing one workspace for calls that run concurrently
  * (on different streams) is a race.  Results are bit-identical run to run.
  * No single counterpart in the reference: it fuses the per-linear launches of
  * int4_triton/gemm.py:245-264 that a decoder block issues back to back

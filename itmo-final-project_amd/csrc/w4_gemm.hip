@@ -27,6 +27,8 @@ int w4_prefill_fast_launch(const void* x, int x_dtype, int64_t M, int64_t N, int
                            void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
 
 // Reference regime boundary: M <= SMALL_M = 64 uses split-K (gemm.py:17, 265).
+int w4_prefill_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M, hipStream_t st);
+
 static constexpr int64_t kSmallM = 64;
 // Decode-shaped products (activations staged in LDS) up to this M.
 static constexpr int64_t kDecodeM = 16;
@@ -107,7 +109,7 @@ static int check_grouped(const w4a16_problem* problems, int count, int64_t M) {
   if (count < 1 || count > W4_MAX_GROUPED)
     return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: count must be in [1, %d]", W4_MAX_GROUPED);
   if (!problems) return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: null problem list");
-  if (M < 1 || M > kDecodeM) return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: M must be in [1, 16]");
+  if (M < 1) return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: M must be >= 1");
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     if (!q.x || !q.qweight || !q.scales || !q.zeros || !q.y)
@@ -123,6 +125,14 @@ static int check_grouped(const w4a16_problem* problems, int count, int64_t M) {
 extern "C" size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, int64_t M) {
   clear_error();
   if (check_grouped(problems, count, M) != W4_OK) return 0;
+  if (M > kDecodeM) {  // room for the separate launches that may replace the shared one
+    size_t most = 0;
+    for (int i = 0; i < count; ++i) {
+      const size_t b = w4a16_workspace_bytes(M, problems[i].N, problems[i].K, problems[i].group_size);
+      most = b > most ? b : most;
+    }
+    return most;
+  }
   const int64_t scratch = w4_gemv_grouped_scratch_bytes(problems, count, M);
   return scratch > 0 ? W4_WORKSPACE_COUNTER_BYTES + (size_t)scratch : 0;
 }
@@ -134,6 +144,20 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
     return fail(W4_ERR_INVALID, "w4a16_gemm_grouped: x dtype must be bf16 or fp16");
   const int rc = check_grouped(problems, count, M);
   if (rc != W4_OK) return rc;
+  if (M > kDecodeM) {
+    // one launch when the products share their activation matrix, else one
+    // w4a16_gemm per problem, in order, on the stream (x rows of K elements)
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int grc = w4_prefill_grouped_launch(problems, count, x_dtype, M, st);
+    if (grc != W4_ERR_UNSUPPORTED || w4_last_error()[0] != '\0') return grc;
+    for (int i = 0; i < count; ++i) {
+      const w4a16_problem& q = problems[i];
+      const int r = w4a16_gemm(q.x, x_dtype, M, q.N, q.K, q.K, 1, q.qweight, q.scales, q.zeros, q.group_size,
+                               q.y, q.N, workspace, workspace_bytes, stream);
+      if (r != W4_OK) return r;
+    }
+    return W4_OK;
+  }
   unsigned* counters;
   void* scratch;
   size_t scratch_bytes;

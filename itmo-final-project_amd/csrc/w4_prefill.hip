@@ -410,7 +410,7 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, 
 }
 
 template <int DT, int NW, bool SZK, int MB>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_kernel(Pf2Args a) {
+__device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   typedef typename Act<DT>::frag F;
   constexpr int BM = 32 * MB;        // rows per tile: MB blocks of 32
   constexpr int XL = BM / 8 / NW;    // direct-to-LDS activation loads per wave per step (1 KB each)
@@ -427,7 +427,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   const int lane = tid & 63;
   const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, lh = lane >> 5;
-  const int t = blockIdx.x;
   const int split = t / a.tiles_mn;
   const int tmn = t - split * a.tiles_mn;
   const int tile_m = tmn / a.tiles_n;
@@ -639,6 +638,30 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
   }
 }
 
+
+template <int DT, int NW, bool SZK, int MB>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_kernel(Pf2Args a) {
+  pf3_tile<DT, NW, SZK, MB>(a, (int)blockIdx.x);
+}
+
+// Several products sharing one activation matrix (q/k/v, gate/up) in one
+// launch: problem p owns workgroups [wg_start[p], wg_start[p + 1]).
+constexpr int PF3_MAX_GROUPED = 4;
+struct Pf3Grouped {
+  Pf2Args prob[PF3_MAX_GROUPED];
+  int wg_start[PF3_MAX_GROUPED + 1];
+  int count;
+};
+
+template <int DT, int NW, bool SZK, int MB>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_grouped_kernel(Pf3Grouped g) {
+  const int b = (int)blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < PF3_MAX_GROUPED; ++i)
+    if (i < g.count && b >= g.wg_start[i]) p = i;
+  pf3_tile<DT, NW, SZK, MB>(g.prob[p], b - g.wg_start[p]);
+}
 }  // namespace w4
 
 using namespace w4host;
@@ -826,4 +849,89 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
   else
     hipLaunchKernelGGL((w4::prefill_kernel<W4_DTYPE_FP16>), grid, block, 0, st, a);
   return check_launch("w4a16_gemm (prefill)");
+}
+
+namespace {
+
+template <int DT, int NW, int MB>
+void pf3_grouped_go(bool szk, const w4::Pf3Grouped& g, int wgs, hipStream_t st) {
+  const dim3 grid((unsigned)wgs), block(NW * 64);
+  if (szk)
+    hipLaunchKernelGGL((w4::pf3_grouped_kernel<DT, NW, true, MB>), grid, block, 0, st, g);
+  else
+    hipLaunchKernelGGL((w4::pf3_grouped_kernel<DT, NW, false, MB>), grid, block, 0, st, g);
+}
+
+template <int DT>
+void pf3_grouped_dt(const Pf2Plan& p, bool szk, const w4::Pf3Grouped& g, int wgs, hipStream_t st) {
+  if (p.nw == 4) {
+    if (p.mb == 4) pf3_grouped_go<DT, 4, 4>(szk, g, wgs, st);
+    else if (p.mb == 2) pf3_grouped_go<DT, 4, 2>(szk, g, wgs, st);
+    else pf3_grouped_go<DT, 4, 1>(szk, g, wgs, st);
+  } else {
+    if (p.mb == 4) pf3_grouped_go<DT, 2, 4>(szk, g, wgs, st);
+    else if (p.mb == 2) pf3_grouped_go<DT, 2, 2>(szk, g, wgs, st);
+    else pf3_grouped_go<DT, 2, 1>(szk, g, wgs, st);
+  }
+}
+
+}  // namespace
+
+// Products that share one dense activation matrix x[M, K] (same pointer, K
+// and group size; x rows of K elements), as one launch of the pipelined
+// kernel.  The tiling is the one the planner picks for the concatenated
+// output width; plans that would split K are left to separate launches.
+// Returns W4_ERR_UNSUPPORTED (nothing launched, no message) when the problems
+// do not qualify.
+int w4_prefill_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M, hipStream_t st) {
+  if (count < 2 || count > w4::PF3_MAX_GROUPED || M < 1) return W4_ERR_UNSUPPORTED;
+  const w4a16_problem& q0 = problems[0];
+  const int64_t K = q0.K, G = q0.group_size;
+  int64_t Nt = 0;
+  for (int i = 0; i < count; ++i) {
+    const w4a16_problem& q = problems[i];
+    if (q.x != q0.x || q.K != K || q.group_size != G || K % w4::PF2_BK != 0 ||
+        !pf2_ok(q.x, M, q.N, K, K, 1, q.qweight, q.scales, q.zeros, q.y, q.N))
+      return W4_ERR_UNSUPPORTED;
+    Nt += q.N;
+  }
+  const Pf2Plan p = plan_pf2(M, Nt, K);
+  if (p.splits != 1) return W4_ERR_UNSUPPORTED;
+  w4::Pf3Grouped g{};
+  const int64_t bm = 32 * p.mb;
+  const int64_t tm = (M + bm - 1) / bm;
+  int wgs = 0;
+  for (int i = 0; i < count; ++i) {
+    const w4a16_problem& q = problems[i];
+    w4::Pf2Args& a = g.prob[i];
+    a.x = static_cast<const uint16_t*>(q.x);
+    a.qw = reinterpret_cast<const uint32_t*>(q.qweight);
+    a.sc = q.scales;
+    a.ze = q.zeros;
+    a.y = static_cast<uint16_t*>(q.y);
+    a.ws = nullptr;
+    a.sxm = K;
+    a.ldy = q.N;
+    a.x_bytes = (uint32_t)(M * K * 2);
+    a.qw_bytes = (uint32_t)((K / 8) * q.N * 4);
+    a.sz_bytes = (uint32_t)((K / G) * q.N * 2);
+    a.M = (int)M;
+    a.N = (int)q.N;
+    a.K = (int)K;
+    a.gshift = ilog2(G);
+    a.tiles_n = (int)((q.N + 64 * p.nw - 1) / (64 * p.nw));
+    a.tiles_mn = (int)(tm * a.tiles_n);
+    a.kt_per_split = (int)(K / w4::PF2_BK);
+    a.y16 = (q.N % 8 == 0 && (uintptr_t)q.y % 16 == 0) ? 1 : 0;
+    g.wg_start[i] = wgs;
+    wgs += a.tiles_mn;
+  }
+  for (int i = count; i <= w4::PF3_MAX_GROUPED; ++i) g.wg_start[i] = wgs;
+  g.count = count;
+  const bool szk = G < 64;
+  if (x_dtype == W4_DTYPE_BF16)
+    pf3_grouped_dt<W4_DTYPE_BF16>(p, szk, g, wgs, st);
+  else
+    pf3_grouped_dt<W4_DTYPE_FP16>(p, szk, g, wgs, st);
+  return check_launch("w4a16_gemm_grouped (prefill)");
 }

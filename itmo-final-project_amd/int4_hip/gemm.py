@@ -100,27 +100,33 @@ def w4a16_matmul(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, z
 
 def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
                          out: Sequence[torch.Tensor] | None = None) -> list[torch.Tensor]:
-    """Several independent small-M products ``xs[i] @ W_i^T`` in ONE kernel launch.
+    """Several independent products ``xs[i] @ W_i^T``, fused into one launch.
 
     ``weights[i]`` is a ``(qweight, scales, zeros)`` triple.  All ``xs[i]`` share
-    dtype and the leading size M (1 <= M <= 16).  This fuses the per-linear
-    decode launches of a transformer block (q/k/v, gate/up, ...); it has no
-    single counterpart in the reference.
+    dtype and the leading size M.  For M <= 16 every problem runs in one decode
+    launch; for larger M, products of one shared activation tensor (q/k/v,
+    gate/up: pass the same tensor) run as one prefill launch when the library's
+    plan allows it, else one launch each.  This fuses the per-linear launches
+    of a transformer block; it has no single counterpart in the reference.
     """
     assert 1 <= len(xs) == len(weights) <= _lib.MAX_GROUPED
     dt = xs[0].dtype
     assert dt in _XDT
     dev = xs[0].device
     M = xs[0].reshape(-1, xs[0].shape[-1]).shape[0]
-    assert 1 <= M <= 16
+    assert M >= 1
     probs = (_lib.Problem * len(xs))()
-    outs, keep = [], []
+    outs, keep, dense = [], [], {}
     for i, (x, (qw, s, z)) in enumerate(zip(xs, weights)):
         assert x.dtype == dt and x.device == dev
         K = x.shape[-1]
-        x2 = x.reshape(-1, K).contiguous()
-        if x2.data_ptr() % 16:
-            x2 = x2.clone()  # the decode kernel reads 16-byte aligned rows
+        # one dense, 16-byte aligned copy per distinct input (shared inputs stay shared)
+        x2 = dense.get(id(x))
+        if x2 is None:
+            x2 = x.reshape(-1, K).contiguous()
+            if x2.data_ptr() % 16:
+                x2 = x2.clone()
+            dense[id(x)] = x2
         assert x2.shape[0] == M and qw.shape[0] * 8 == K
         G = _check_weight(qw, s, z, K)
         qw, s, z = qw.contiguous(), s.contiguous(), z.contiguous()

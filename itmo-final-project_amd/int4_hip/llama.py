@@ -21,9 +21,9 @@ Attention is computed in fp32 from contiguous operands: the KV cache is fp32
 and keeps K transposed ([kv_heads, head_dim, positions]), so no bf16 batched
 product with a transposed operand is issued.
 
-Decode steps with Int4Linear projections issue q/k/v as one grouped W4A16
-launch into one buffer and gate/up as another (``w4a16_matmul_grouped``), so a
-layer makes 4 W4A16 launches instead of 7.
+With Int4Linear projections, q/k/v (into one buffer when decoding) and
+gate/up each go through one grouped W4A16 call (``w4a16_matmul_grouped``), so
+a layer makes 4 W4A16 launches instead of 7.
 """
 from __future__ import annotations
 
@@ -92,18 +92,17 @@ def _all_int4(mods) -> bool:
     return all(isinstance(m, Int4Linear) for m in mods) and len({m.group_size for m in mods}) == 1
 
 
-def _grouped(x: torch.Tensor, mods) -> torch.Tensor:
-    """Outputs of several Int4Linear (no bias) on one small-M input, side by side in one
-    [M, sum N] buffer, from one grouped W4A16 launch."""
+def _grouped(x: torch.Tensor, mods, buf: torch.Tensor | None = None) -> list:
+    """Outputs of several Int4Linear (no bias) on one input from one grouped W4A16
+    call; with ``buf`` (a single row, [1, sum N]) they are slices of it."""
     from .gemm import w4a16_matmul_grouped
-    sizes = [m.out_features for m in mods]
-    buf = torch.empty((x.shape[0], sum(sizes)), dtype=x.dtype, device=x.device)
-    outs, o = [], 0
-    for n in sizes:
-        outs.append(buf[:, o:o + n])
-        o += n
-    w4a16_matmul_grouped([x] * len(mods), [(m.qweight, m.scales, m.zeros) for m in mods], out=outs)
-    return buf
+    outs = None
+    if buf is not None:
+        outs, o = [], 0
+        for m in mods:
+            outs.append(buf[:, o:o + m.out_features])
+            o += m.out_features
+    return w4a16_matmul_grouped([x] * len(mods), [(m.qweight, m.scales, m.zeros) for m in mods], out=outs)
 
 
 class Attention(nn.Module):
@@ -123,10 +122,12 @@ class Attention(nn.Module):
         nq, nk = self.nh * self.d, self.nkv * self.d
         g = self.nh // self.nkv
         scale = 1.0 / math.sqrt(self.d)
+        mods = (self.q_proj, self.k_proj, self.v_proj)
         if pos_t is None:
-            q = apply_rope(self.q_proj(x).view(T, self.nh, self.d), cos, sin)
-            k = apply_rope(self.k_proj(x).view(T, self.nkv, self.d), cos, sin)
-            v = self.v_proj(x).view(T, self.nkv, self.d)
+            qo, ko, vo = _grouped(x, mods) if _all_int4(mods) else [m(x) for m in mods]
+            q = apply_rope(qo.view(T, self.nh, self.d), cos, sin)
+            k = apply_rope(ko.view(T, self.nkv, self.d), cos, sin)
+            v = vo.view(T, self.nkv, self.d)
             kc[:, :, pos0:pos0 + T] = k.permute(1, 2, 0)
             vc[:, pos0:pos0 + T] = v.transpose(0, 1)
             L = pos0 + T
@@ -140,9 +141,9 @@ class Attention(nn.Module):
             o = torch.bmm(torch.softmax(s, dim=-1), vv)                   # [kv, g*T, D]
             o = o.view(self.nkv, g, T, self.d).permute(2, 0, 1, 3).reshape(T, nq)
         else:
-            mods = (self.q_proj, self.k_proj, self.v_proj)
             if _all_int4(mods):
-                qkv = _grouped(x, mods)
+                qkv = torch.empty((1, nq + 2 * nk), dtype=x.dtype, device=x.device)
+                _grouped(x, mods, qkv)
             else:
                 qkv = torch.cat([m(x) for m in mods], dim=-1)
             qk = apply_rope(qkv[:, :nq + nk].view(1, self.nh + self.nkv, self.d), cos, sin)[0]
@@ -162,10 +163,9 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(i, h, bias=False)
 
     def forward(self, x):
-        if x.shape[0] <= 16 and _all_int4((self.gate_proj, self.up_proj)):
-            gu = _grouped(x, (self.gate_proj, self.up_proj))
-            n = self.gate_proj.out_features
-            return self.down_proj(F.silu(gu[:, :n]) * gu[:, n:])
+        if _all_int4((self.gate_proj, self.up_proj)):
+            g, u = _grouped(x, (self.gate_proj, self.up_proj))
+            return self.down_proj(F.silu(g) * u)
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 

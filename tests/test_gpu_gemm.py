@@ -271,3 +271,26 @@ def test_prefill_split_k_bit_identical(M, NK):
     _check(out, x, qw, s, z, ref_unrounded=False)
     for _ in range(2):
         assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
+
+
+# grouped products for M > 16: a shared activation runs as one prefill launch
+# when the plan for the concatenated width needs no split-K (these shapes), a
+# mix of inputs falls back to one launch per problem; every output against the
+# oracle, repeat calls bit-identical
+@pytest.mark.parametrize("G", [32, 128])
+@pytest.mark.parametrize("M,K,Ns", [(130, 512, (256, 64, 64)), (300, 256, (1024, 256, 256)),
+                                     (512, 512, (192, 72, 120)), (40, 512, (128, 64))])
+def test_grouped_shared_activation(M, K, Ns, G):
+    print(f"[grouped-prefill] M={M} K={K} Ns={Ns} G={G}", flush=True)
+    ws = [_weights(N, K, G, seed=400 + i) for i, N in enumerate(Ns)]
+    x = randn((M, K), seed=410 + M).to(DEV)
+    outs = int4_hip.w4a16_matmul_grouped([x] * len(Ns), ws)
+    for (qw, s, z), y in zip(ws, outs):
+        _check(y, x, qw, s, z)
+    again = int4_hip.w4a16_matmul_grouped([x] * len(Ns), ws)
+    for a, b in zip(outs, again):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    xs = [randn((M, K), seed=420 + i).to(DEV) for i in range(len(Ns))]
+    mixed = int4_hip.w4a16_matmul_grouped(xs, ws)
+    for xi, (qw, s, z), y in zip(xs, ws, mixed):
+        _check(y, xi, qw, s, z)
