@@ -65,6 +65,32 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         return ws
 
 
+_WS_BYTES: dict = {}
+
+
+def _ws_bytes(lib, M: int, N: int, K: int, G: int) -> int:
+    """Workspace size of one product; a pure function of the shape, memoised."""
+    key = (M, N, K, G)
+    b = _WS_BYTES.get(key)
+    if b is None:
+        b = _WS_BYTES[key] = lib.w4a16_workspace_bytes(M, N, K, G)
+    return b
+
+
+def _gemm_call(lib, x2, dt, M, N, K, qweight, scales, zeros, G, y, device):
+    # torch's raw current-stream query is a fraction of the cost of
+    # torch.cuda.current_stream(); the library reads the current device (for
+    # its CU count), which the caller has made the tensors' device
+    stream = torch._C._cuda_getCurrentRawStream(device.index)
+    nb = _ws_bytes(lib, M, N, K, G)
+    ws = _workspace(device, stream, nb) if nb else None
+    return lib.w4a16_gemm(
+        x2.data_ptr(), dt, M, N, K, x2.stride(0), x2.stride(1),
+        qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(), G,
+        y.data_ptr(), N, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
+        stream)
+
+
 def w4a16_matmul(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor) -> torch.Tensor:
     """x[..., K] (bf16/fp16) @ W^T, W given as packed int4 (see quantize.py). Returns x.dtype [..., N].
 
@@ -74,28 +100,24 @@ def w4a16_matmul(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, z
     K = x.shape[-1]
     assert qweight.shape[0] * 8 == K, (qweight.shape, K)
     G = _check_weight(qweight, scales, zeros, K)
-    assert x.is_cuda and qweight.device == x.device and scales.device == x.device and zeros.device == x.device
+    dev = x.device
+    assert x.is_cuda and qweight.device == dev and scales.device == dev and zeros.device == dev
     N = qweight.shape[1]
     x2 = x.reshape(-1, K)
     M = x2.shape[0]
     qweight, scales, zeros = qweight.contiguous(), scales.contiguous(), zeros.contiguous()
-    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    y = torch.empty((M, N), dtype=x.dtype, device=dev)
     if M == 0 or N == 0:
         return y.reshape(*x.shape[:-1], N)
     lib = _lib.load()
-    with torch.cuda.device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
-        ws_bytes = lib.w4a16_workspace_bytes(M, N, K, G)
-        ws = _workspace(x.device, stream, ws_bytes) if ws_bytes else None
-        rc = lib.w4a16_gemm(
-            x2.data_ptr(), _XDT[x.dtype], M, N, K, x2.stride(0), x2.stride(1),
-            qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(), G,
-            y.data_ptr(), N, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
-            stream)
-    _lib.check(rc, "w4a16_gemm")
+    if torch._C._cuda_getDevice() == dev.index:
+        rc = _gemm_call(lib, x2, _XDT[x.dtype], M, N, K, qweight, scales, zeros, G, y, dev)
+    else:
+        with torch.cuda.device(dev):
+            rc = _gemm_call(lib, x2, _XDT[x.dtype], M, N, K, qweight, scales, zeros, G, y, dev)
+    if rc:
+        _lib.check(rc, "w4a16_gemm")
     return y.reshape(*x.shape[:-1], N)
-
-
 
 
 def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
@@ -137,13 +159,21 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
         keep += [x2, qw, s, z]
         outs.append(y)
     lib = _lib.load()
-    with torch.cuda.device(dev):
-        stream = torch.cuda.current_stream(dev).cuda_stream
+
+    def call():
+        stream = torch._C._cuda_getCurrentRawStream(dev.index)
         nbytes = lib.w4a16_grouped_workspace_bytes(probs, len(xs), M)
         ws = _workspace(dev, stream, nbytes) if nbytes else None
-        rc = lib.w4a16_gemm_grouped(probs, len(xs), _XDT[dt], M, ws.data_ptr() if ws is not None else None,
-                                    ws.numel() if ws is not None else 0, stream)
-    _lib.check(rc, "w4a16_gemm_grouped")
+        return lib.w4a16_gemm_grouped(probs, len(xs), _XDT[dt], M, ws.data_ptr() if ws is not None else None,
+                                      ws.numel() if ws is not None else 0, stream)
+
+    if torch._C._cuda_getDevice() == dev.index:
+        rc = call()
+    else:
+        with torch.cuda.device(dev):
+            rc = call()
+    if rc:
+        _lib.check(rc, "w4a16_gemm_grouped")
     return [y.reshape(*x.shape[:-1], y.shape[-1]) for x, y in zip(xs, outs)]
 
 
