@@ -142,6 +142,47 @@ def cpu_baseline(packed, xs_bits, sample_passes: int) -> dict:
             "ms_per_block": round(t * 1e3, 3)}
 
 
+def cpu_quantize_baseline(w_bits, q_bytes: int, passes: int) -> dict:
+    """The CPU oracle's quantize_int4 (numpy port of the reference's
+    quantize_int4_ref) over the 7 block weights (bf16 bits as numpy)."""
+    import numpy as np
+
+    from oracle import w4a16_oracle as O
+
+    ts = []
+    for _ in range(passes):
+        t0 = time.perf_counter()
+        for w in w_bits:
+            O.quantize_int4(w, "bf16", G)
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    return {"value": round(q_bytes / t / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"numpy oracle quantize_int4 over the 7 block weights (G=128, bf16), "
+                      f"median of {passes} passes ({t * 1e3:.1f} ms per block)",
+            "ms_per_block": round(t * 1e3, 3)}
+
+
+def device_copy_gbps(dev, stream, nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """Measured HBM rate of a plain device-to-device copy (read + write bytes
+    over time), beside the 8 TB/s datasheet peak the roofline uses."""
+    import torch
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            dst.copy_(src)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            dst.copy_(src)
+        e1.record(stream)
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
 PROFILE = ROOT / "profiles" / "dec_kernel_one_decode_block_m1.md"
 ROOFLINE_KERNEL = "dec_kernel_one<0, 2>"
 
@@ -218,6 +259,9 @@ def main() -> int:
     ap.add_argument("--only", default="all",
                     help="comma list of sections to run: decode, perlinear, splitk, prefill, quantize, llama "
                          "(profiling runs use one section; the JSON line needs 'decode')")
+    ap.add_argument("--small-m", default="2,4,8,16,32,64",
+                    help="comma list of M for the small-M section (profiling runs may pick one)")
+    ap.add_argument("--small-g", default="128,64,32", help="comma list of group sizes for the small-M section")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run one 32 MiB device copy (for scaling FETCH_SIZE/WRITE_SIZE counters)")
     ap.add_argument("--summarize-prof", default=None, metavar="DIR",
@@ -272,6 +316,8 @@ def main() -> int:
         gq = graph_of(lambda: [quant_set(i)() for i in range(nsets)], stream)
         q_ms = time_graph(gq, 3, stream) / nsets
         del gq
+    # the first set's bf16 weights, kept on the host for the CPU quantize baseline
+    w16_host = [w.cpu() for w in w16[0]] if ("quantize" in only and not args.no_cpu) else None
     del w16
     torch.cuda.empty_cache()
 
@@ -328,7 +374,7 @@ def main() -> int:
     # weight sets (G=128 reuses the decode sets; G=64/32 are quantized here)
     ms16, small = None, {}
     if "splitk" in only:
-        for g in (128, 64, 32):
+        for g in [int(v) for v in args.small_g.split(",")]:
             if g == G:
                 packs = packed
             else:
@@ -341,7 +387,7 @@ def main() -> int:
                         del w
                     packs.append(one)
             small[g] = {}
-            for M in (2, 4, 8, 16, 32, 64):
+            for M in [int(v) for v in args.small_m.split(",")]:
                 xsm = [torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16) for _, N, K in LINEARS]
                 gm = graph_of(lambda: [int4_hip.w4a16_matmul(xsm[j], *packs[i][j]) for i in range(nsets)
                                        for j in range(len(LINEARS))], stream)
@@ -414,12 +460,15 @@ def main() -> int:
         torch.cuda.synchronize()
 
     # ------------------------------------------------- CPU baseline (rank 0, N=1)
-    cpu = None
+    cpu = cpu_q = None
     if not args.no_cpu:
         def bits(t):
             return t.contiguous().view(torch.int16).numpy().view(np.uint16)
         packed0 = [(qw.cpu().numpy(), bits(s.cpu()), bits(z.cpu())) for qw, s, z in packed[0]]
         cpu = cpu_baseline(packed0, [bits(x.cpu()) for x in xs1[0]], args.cpu_passes)
+        if "quantize" in only:
+            cpu_q = cpu_quantize_baseline([bits(w) for w in w16_host], q_bytes, 3)
+    copy_gbps = device_copy_gbps(dev, stream) if "decode" in only else None
 
     traffic = profiled_traffic()
     out = {
@@ -463,6 +512,8 @@ def main() -> int:
         "prefill_m2048_mfma_frac": round(pre[2048]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4) if pre else None,
         "quantize_us_per_block": round(q_ms * 1e3, 2) if q_ms else None,
         "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None,
+        "cpu_baseline_quantize": cpu_q,
+        "hbm_device_copy_gbps": round(copy_gbps, 1) if copy_gbps else None,
         "llama_1b_w4": llama,
         "device": torch.cuda.get_device_name(dev),
     }

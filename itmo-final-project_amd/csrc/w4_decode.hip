@@ -199,10 +199,16 @@ struct DecChunk {
 //        8-element k slice each), are permuted once and shared through LDS;
 //        all 16 rows of the MFMA operand repeat row 0, so only element 0 of
 //        each accumulator is corrected and reduced.
-//   !ONE: rows 0..M-1 (lanes with c >= M repeat row M-1); each lane loads and
-//        permutes its own fragment every step.
+//   !ONE: rows 0..M-1 (M <= MX; lanes with c >= M repeat row M-1).  A
+//        chunk's activations (M rows x 4C 16-byte k slices, each row a
+//        contiguous 64C-byte run) travel with it as XL = MX*C/16 coalesced
+//        loads per wave (entry f = 64 j + lane: row f / 4C, slice f % 4C);
+//        they are permuted once and staged in the wave's own LDS area, slice
+//        s of row m at slot 4C m + (s ^ m), so both the staging writes and the
+//        per-step fragment reads (16 rows of one slice) are free of bank
+//        conflicts.
 // GS = correction interval in steps (min(group size / 32, C)).
-template <int DT, int VEC, bool ONE, int GS>
+template <int DT, int VEC, bool ONE, int GS, int MX>
 __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red, uint32_t* xl) {
   typedef typename Act<DT>::frag F;
   typedef DecNum<DT> Num;
@@ -212,7 +218,10 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   constexpr int D = DecChunk<VEC>::D;
   constexpr int NP = C / GS;  // correction points per chunk
   constexpr int R = ONE ? 1 : 4;
+  constexpr int C4 = 4 * C;              // 16-byte activation slices per row and chunk
+  constexpr int XL = ONE ? 1 : MX * C / 16;  // activation loads per chunk and lane
   static_assert(GS >= 1 && GS <= C && (C % GS) == 0, "correction interval");
+  static_assert(ONE || (XL >= 1 && MX <= C4 && MX <= 16), "activation staging");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -238,16 +247,30 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   const uint32_t col = (uint32_t)(n0 + VEC * c);
   const uint32_t w_lane = ((uint32_t)kb * (uint32_t)N + col) * 4u;
   const uint32_t sz_lane = col * 2u;
-  // ONE: lane l < 4C carries k8 row 4*sb + l of the chunk; !ONE: own row, own kb
-  const uint32_t x_lane = ONE ? (uint32_t)lane * 16u
-                              : (uint32_t)((int64_t)min(c, M - 1) * a.sxm * 2) + (uint32_t)kb * 16u;
+  // ONE: lane l < 4C carries k8 row 4*sb + l of the chunk
+  const uint32_t x_lane = (uint32_t)lane * 16u;
+  // !ONE: load j carries entry f = 64 j + lane = (row f / 4C, slice f % 4C);
+  // rows >= M are out of range (no traffic), so are slices past K (zeros)
+  uint32_t x_off[XL];
+  int x_step[XL];
+  if constexpr (!ONE) {
+#pragma unroll
+    for (int j = 0; j < XL; ++j) {
+      const int f = 64 * j + lane;
+      const int m = f / C4, sl = f % C4;
+      x_step[j] = sl >> 2;
+      x_off[j] = m < M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)sl * 16u : kDecOOB;
+    }
+  }
+  const int mc = min(c, M - 1);
+  const int x_rd = mc * C4 + (kb ^ mc);  // read slot of step 0; step st adds 4 st inside the XOR
   const uint32_t magic = dec_magic_vgpr<DT>();
   const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
 
   struct Chunk {
     WT w[C];
     DecH<VEC> s[NP], z[NP];
-    u32x4 xv[ONE ? 1 : C];
+    u32x4 xv[XL];
   };
 
   // Out-of-range offsets are formed by OR-ing bit 31 in (never by selecting
@@ -263,6 +286,14 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
       const uint32_t xo = ((uint32_t)sb * 64u + x_lane) | x_lane_oob | oob;
       ch.xv[0] = __builtin_amdgcn_raw_buffer_load_b128(rx, xo, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
+    } else {
+#pragma unroll
+      for (int j = 0; j < XL; ++j) {
+        // slices of steps past K read 0 (the next row must not leak in)
+        const uint32_t xoob = sb + x_step[j] < S ? oob : kDecOOB;
+        ch.xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, ((uint32_t)sb * 64u + x_off[j]) | xoob, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -274,14 +305,7 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t vo = ((uint32_t)sb * step_bytes + w_lane) | oob;
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-      ch.w[i] = DecW<VEC>::load(rq, vo + (uint32_t)i * step_bytes);
-      if constexpr (!ONE) {
-        // steps past K read 0 (rows of other activations must not leak in)
-        const uint32_t xoob = sb + i < S ? oob : kDecOOB;
-        ch.xv[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ((uint32_t)(sb + i) * 64u + x_lane) | xoob, 0, 0);
-      }
-    }
+    for (int i = 0; i < C; ++i) ch.w[i] = DecW<VEC>::load(rq, vo + (uint32_t)i * step_bytes);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -299,6 +323,15 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
       const u32x4 v = dec_perm_x(ch.xv[0]);
       *reinterpret_cast<u32x4*>(xl + (wv * 64 + lane) * 4) = v;
       __builtin_amdgcn_wave_barrier();
+    } else {
+      // stage this chunk's activations in the wave's area, permuted
+#pragma unroll
+      for (int j = 0; j < XL; ++j) {
+        const int f = 64 * j + lane;
+        const int m = f / C4, sl = f % C4;
+        *reinterpret_cast<u32x4*>(xl + (wv * MX * C4 + m * C4 + (sl ^ m)) * 4) = dec_perm_x(ch.xv[j]);
+      }
+      __builtin_amdgcn_wave_barrier();
     }
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
@@ -309,7 +342,8 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
         if constexpr (ONE)
           xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(xl + (wv * 64 + st * 4 + kb) * 4));
         else
-          xa = __builtin_bit_cast(F, dec_perm_x(ch.xv[st]));
+          xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(
+                                         xl + (wv * MX * C4 + (x_rd ^ (4 * st))) * 4));
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
           const F b = __builtin_bit_cast(F, Num::bvals(DecW<VEC>::get(ch.w[st], j), magic));
@@ -329,7 +363,7 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
         }
       }
     }
-    if constexpr (ONE) __builtin_amdgcn_wave_barrier();  // slots are rewritten by the next chunk
+    __builtin_amdgcn_wave_barrier();  // slots are rewritten by the next chunk
   };
 
   // Ring of D chunks: chunk t + D is loaded as soon as chunk t is consumed.
@@ -347,14 +381,18 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
     }
   }
 
-  // cross-wave reduction in wave order
+  // cross-wave reduction in wave order; !ONE: each wave's partial tile goes
+  // to its own activation area, which no other wave touches and which the
+  // wave itself no longer reads
+  float* const rbase = ONE ? red : reinterpret_cast<float*>(xl);
+  const int rstride = ONE ? M * TN : MX * C4 * 4;
   if (ONE ? kb == 0 : true) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int m = ONE ? 0 : kb * 4 + r;
       if (m < M) {
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) red[(wv * M + m) * TN + VEC * c + j] = tot[j][r];
+        for (int j = 0; j < VEC; ++j) rbase[wv * rstride + m * TN + VEC * c + j] = tot[j][r];
       }
     }
   }
@@ -365,9 +403,9 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
     const int nl = idx - m * TN;
     const int n = n0 + nl;
     if (n >= N) continue;
-    float s = red[m * TN + nl];
+    float s = rbase[m * TN + nl];
 #pragma unroll
-    for (int w = 1; w < kDecWaves; ++w) s += red[(w * M + m) * TN + nl];
+    for (int w = 1; w < kDecWaves; ++w) s += rbase[w * rstride + m * TN + nl];
     a.y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(s * (1.0f / Num::QS));
   }
 }
@@ -600,7 +638,7 @@ __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) 
   }
 }
 
-template <int DT, bool ONE, int GS>
+template <int DT, bool ONE, int GS, int MX>
 __global__ __launch_bounds__(kDecThreads) void dec_kernel(DecGroupedArgs g) {
   extern __shared__ __attribute__((aligned(16))) float dec_smem[];
   const int t = blockIdx.x;
@@ -610,15 +648,16 @@ __global__ __launch_bounds__(kDecThreads) void dec_kernel(DecGroupedArgs g) {
     if (i < g.count && t >= g.wg_start[i]) p = i;
   const DecArgs& a = g.prob[p];
   const int tile = t - g.wg_start[p];
-  // LDS: [activation slots, ONE only: 8 waves x 64 x 16 B][reduction]
+  // LDS, ONE: [activation slots: 8 waves x 64 x 16 B][reduction: 8 waves x 64 floats];
+  // !ONE: [activation areas: 8 waves x MX x 4C x 16 B], reused for the reduction
   uint32_t* xl = reinterpret_cast<uint32_t*>(dec_smem);
-  float* red = dec_smem + (ONE ? kDecWaves * 64 * 4 : 0);
+  float* red = dec_smem + kDecWaves * 64 * 4;
   if (a.vec == 4)
-    dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4)>(a, tile, red, xl);
+    dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4), MX>(a, tile, red, xl);
   else if (a.vec == 2)
-    dec_tile<DT, 2, ONE, GS>(a, tile, red, xl);
+    dec_tile<DT, 2, ONE, GS, MX>(a, tile, red, xl);
   else
-    dec_tile<DT, 1, ONE, GS>(a, tile, red, xl);
+    dec_tile<DT, 1, ONE, GS, MX>(a, tile, red, xl);
 }
 
 }  // namespace w4
@@ -636,6 +675,7 @@ struct DecPlan {
   w4::DecGroupedArgs g;
   int wgs;
   int gs;         // group-size class of the chosen kernel
+  int mx;         // dec_kernel, M > 1: activation rows staged per wave (4, 8 or 16)
   bool cu_tiles;  // M == 1 one-workgroup-per-CU kernel (dec_kernel_one)
   int threads;
   size_t lds;
@@ -756,7 +796,13 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   } else {
     dp.gs = (int)std::min(G / 32, 8);  // dec_kernel: steps per group, capped at 8
     dp.threads = w4::kDecThreads;
-    dp.lds = (M == 1 ? (size_t)w4::kDecWaves * 64 * 16 : 0) + (size_t)w4::kDecWaves * M * 64 * sizeof(float);
+    dp.mx = M <= 4 ? 4 : M <= 8 ? 8 : 16;
+    bool narrow = false;  // a tile of vec < 4 has chunks of 8 steps (32 slices per row)
+    for (int s = 0; s < count; ++s) narrow = narrow || dp.g.prob[s].vec < 4;
+    // ONE: activation slots + reduction; M > 1: activation areas (at most
+    // 64 KB), which also hold the per-wave partial tiles (M x 64 floats <= MX x 4C x 16 B)
+    dp.lds = M == 1 ? (size_t)w4::kDecWaves * 64 * 16 + (size_t)w4::kDecWaves * 64 * sizeof(float)
+                    : (size_t)w4::kDecWaves * dp.mx * (narrow ? 32 : 16) * 16;
   }
   return wgs > 0;
 }
@@ -773,14 +819,14 @@ void dec_launch_one(const DecPlan& dp, hipStream_t st) {
   }
 }
 
-template <int DT, bool ONE>
+template <int DT, bool ONE, int MX>
 void dec_launch_generic(const DecPlan& dp, hipStream_t st) {
   const dim3 grid((unsigned)dp.wgs), block(w4::kDecThreads);
   switch (dp.gs) {
-    case 1: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 1>), grid, block, dp.lds, st, dp.g); break;
-    case 2: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 2>), grid, block, dp.lds, st, dp.g); break;
-    case 4: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 4>), grid, block, dp.lds, st, dp.g); break;
-    default: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 8>), grid, block, dp.lds, st, dp.g); break;
+    case 1: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 1, MX>), grid, block, dp.lds, st, dp.g); break;
+    case 2: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 2, MX>), grid, block, dp.lds, st, dp.g); break;
+    case 4: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 4, MX>), grid, block, dp.lds, st, dp.g); break;
+    default: hipLaunchKernelGGL((w4::dec_kernel<DT, ONE, 8, MX>), grid, block, dp.lds, st, dp.g); break;
   }
 }
 
@@ -789,9 +835,13 @@ void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
   if (dp.cu_tiles)
     dec_launch_one<DT>(dp, st);
   else if (M == 1)
-    dec_launch_generic<DT, true>(dp, st);
+    dec_launch_generic<DT, true, 1>(dp, st);
+  else if (dp.mx == 4)
+    dec_launch_generic<DT, false, 4>(dp, st);
+  else if (dp.mx == 8)
+    dec_launch_generic<DT, false, 8>(dp, st);
   else
-    dec_launch_generic<DT, false>(dp, st);
+    dec_launch_generic<DT, false, 16>(dp, st);
 }
 
 }  // namespace
