@@ -19,10 +19,93 @@ __device__ __forceinline__ float clamp_nan(float x, float lo, float hi) {
   return (x != x) ? x : fminf(fmaxf(x, lo), hi);
 }
 
+// NaN-propagating maximum / minimum (v_maximum3_f32 / v_minimum3_f32 on
+// gfx950): a NaN anywhere in a group reaches the reduced extremes, as with
+// torch's amax / amin (quantize.py:108-109); no input canonicalization.
+__device__ __forceinline__ float fmax_p(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float fmin_p(float a, float b) { return __builtin_elementwise_minimum(a, b); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, true));
+}
+
+// Maximum and minimum over aligned groups of L lanes (L a power of two up to
+// 64): DPP steps inside rows of 16 lanes (swap neighbours, swap pairs,
+// half-row mirror, row mirror), lane shuffles across rows.
+template <int L>
+__device__ __forceinline__ void group_minmax(float& mx, float& mn) {
+  if constexpr (L >= 2) {
+    mx = fmax_p(mx, dpp_mov<0xB1>(mx));  // quad_perm [1,0,3,2]
+    mn = fmin_p(mn, dpp_mov<0xB1>(mn));
+  }
+  if constexpr (L >= 4) {
+    mx = fmax_p(mx, dpp_mov<0x4E>(mx));  // quad_perm [2,3,0,1]
+    mn = fmin_p(mn, dpp_mov<0x4E>(mn));
+  }
+  if constexpr (L >= 8) {
+    mx = fmax_p(mx, dpp_mov<0x141>(mx));  // row_half_mirror
+    mn = fmin_p(mn, dpp_mov<0x141>(mn));
+  }
+  if constexpr (L >= 16) {
+    mx = fmax_p(mx, dpp_mov<0x140>(mx));  // row_mirror
+    mn = fmin_p(mn, dpp_mov<0x140>(mn));
+  }
+  if constexpr (L >= 32) {
+    mx = fmax_p(mx, __shfl_xor(mx, 16, 64));
+    mn = fmin_p(mn, __shfl_xor(mn, 16, 64));
+  }
+  if constexpr (L >= 64) {
+    mx = fmax_p(mx, __shfl_xor(mx, 32, 64));
+    mn = fmin_p(mn, __shfl_xor(mn, 32, 64));
+  }
+}
+
 struct QStats {
   float scale;  // fp16-representable (or 0/inf/NaN in degenerate groups)
   float zero;
 };
+
+// Fast form of group_stats, bit-identical to it, plus rcp(scale).
+//  - scale: for x = wmax - wmin in [2^-90, 2^126], y = x * fl(1/15) followed
+//    by one fma correction with the exact residual fma(-y, 15, x) is the
+//    correctly rounded x / 15 (checked for every float in that range by
+//    tests/div15_exhaustive.c); elsewhere the IEEE division.
+//  - zero: -wmin / scale <= 22.5 (scale >= x / 15 up to the fp16 rounding,
+//    which for a subnormal scale >= 2^-24 is at most 2^-25), so with
+//    v_rcp_f32 within 1 ulp t0 = fma(-wmin, rcp(scale), 0.5) is within 6e-6
+//    of the reference's fl(fl(-wmin / scale) + 0.5) and the floors agree
+//    unless fract(t0) is within 2^-15 of 0 or 1, where, and for a zero /
+//    infinite / NaN scale, the IEEE division is used.
+__device__ __forceinline__ QStats group_stats_fast(float rmax, float rmin, float* rcp) {
+#pragma clang fp contract(off)
+  const float wmax = max_nan(rmax, 0.0f);
+  const float wmin = min_nan(rmin, 0.0f);
+  const float x = wmax - wmin;
+  float scale;
+  if (x >= 0x1p-90f && x <= 0x1p126f) {
+    constexpr float C15 = 1.0f / 15.0f;
+    const float y = x * C15;
+    scale = __builtin_fmaf(__builtin_fmaf(-y, 15.0f, x), C15, y);
+  } else {
+    scale = x / 15.0f;
+  }
+  if (scale == 0.0f) scale = 1.0f;
+  scale = (float)(_Float16)scale;
+  const float r = __builtin_amdgcn_rcpf(scale);
+  const float t0 = __builtin_fmaf(-wmin, r, 0.5f);
+  const float f0 = __builtin_amdgcn_fractf(t0);
+  float zero;
+  if (scale > 0.0f && scale < __builtin_inff() && f0 >= 0x1p-15f && f0 <= 1.0f - 0x1p-15f)
+    zero = __builtin_amdgcn_fmed3f(floorf(t0), 0.0f, 15.0f);
+  else
+    zero = clamp_nan(floorf(-wmin / scale + 0.5f), 0.0f, 15.0f);
+  *rcp = r;
+  QStats st;
+  st.scale = scale;
+  st.zero = zero;
+  return st;
+}
 
 // quantize.py:108-112, in the same fp32 op order (true IEEE division).
 __device__ __forceinline__ QStats group_stats(float rmax, float rmin) {
@@ -60,21 +143,23 @@ __device__ __forceinline__ uint32_t quantize_pack8(const float v[8], QStats st) 
 // so while |w/scale| < 32, t lies within 8e-6 of the reference's
 // fl(fl(w/scale) + 0.5) + zero and both floors agree unless t is within 2^-15
 // of an integer; beyond that range both clamp to the same end (0 or 15).
-// *dev returns max |frac(t) - 1/2| over the word: above 1/2 - 2^-15 the
-// caller repacks the word with quantize_pack8.  Otherwise the word is
-// bit-identical to quantize_pack8's.
-__device__ __forceinline__ uint32_t quantize_pack8_fast(const float v[8], QStats st, float rcp, float* dev) {
+// q = trunc(med3(t, 0, 15.5)) is clamp(floor(t), 0, 15).  Returns true in
+// *near when some fract(t) is within 2^-15 of 0 or 1: the caller then repacks
+// the word with quantize_pack8.  Otherwise the word is bit-identical to
+// quantize_pack8's.
+__device__ __forceinline__ uint32_t quantize_pack8_fast(const float v[8], QStats st, float rcp, bool* near) {
   const float c = 0.5f + st.zero;
   uint32_t word = 0;
-  float m = 0.0f;
+  float lo = 1.0f, hi = 0.0f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const float t = __builtin_fmaf(v[i], rcp, c);
-    const float f = floorf(t);
-    m = fmaxf(m, fabsf((t - f) - 0.5f));
-    word |= (uint32_t)__builtin_amdgcn_fmed3f(f, 0.0f, 15.0f) << (4 * i);
+    const float f = __builtin_amdgcn_fractf(t);
+    lo = fmin_p(lo, f);
+    hi = fmax_p(hi, f);
+    word |= (uint32_t)__builtin_amdgcn_fmed3f(t, 0.0f, 15.5f) << (4 * i);
   }
-  *dev = m;
+  *near = !(lo >= 0x1p-15f && hi <= 1.0f - 0x1p-15f);
   return word;
 }
 
@@ -179,72 +264,34 @@ __global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
                          e[4] | ((uint32_t)e[5] << 16), e[6] | ((uint32_t)e[7] << 16)};
         }
       }
-      // One ballot per batch: without a NaN anywhere in it, plain min/max (the
-      // sign of a zero extreme does not reach group_stats' result) and the
-      // reciprocal packing, redone exactly for the rare flagged words.
-      bool has_nan = false;
+      // NaN-propagating extremes: a group without NaN takes the reciprocal
+      // packing, redone exactly for the rare flagged words; a group with a
+      // NaN (NaN extremes) takes the exact path (the sign of a zero extreme
+      // does not reach group_stats' result)
 #pragma unroll
-      for (int i = 0; i < B; ++i)
+      for (int i = 0; i < B; ++i) {
+        const int row = sub * RW + (b0 + i) * RPI + rsub;
+        float v[8];
+        unpack_row8<DT>(raw[i], v);
+        float mx = fmax_p(v[0], v[1]), mn = fmin_p(v[0], v[1]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          has_nan |= act_bits_to_float((uint16_t)(raw[i][j] & 0xFFFFu), DT) !=
-                     act_bits_to_float((uint16_t)(raw[i][j] & 0xFFFFu), DT);
-          has_nan |= act_bits_to_float((uint16_t)(raw[i][j] >> 16), DT) !=
-                     act_bits_to_float((uint16_t)(raw[i][j] >> 16), DT);
+        for (int j = 2; j < 8; ++j) {
+          mx = fmax_p(mx, v[j]);
+          mn = fmin_p(mn, v[j]);
         }
-      if (__builtin_amdgcn_ballot_w64(has_nan) == 0) {
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-          const int row = sub * RW + (b0 + i) * RPI + rsub;
-          float v[8];
-          unpack_row8<DT>(raw[i], v);
-          float mx = v[0], mn = v[0];
-#pragma unroll
-          for (int j = 1; j < 8; ++j) {
-            mx = fmaxf(mx, v[j]);
-            mn = fminf(mn, v[j]);
-          }
-#pragma unroll
-          for (int off = L / 2; off > 0; off >>= 1) {
-            mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            mn = fminf(mn, __shfl_xor(mn, off, 64));
-          }
-          const QStats st = group_stats(mx, mn);
-          float dev;
-          uint32_t word = quantize_pack8_fast(v, st, __builtin_amdgcn_rcpf(st.scale), &dev);
-          // near a rounding boundary, or an infinite weight (infinite scale)
-          // or a scale rounded to 0 in fp16: the exact path
-          if (!(dev <= 0.5f - 1.0f / 32768.0f) || !(st.scale > 0.0f && st.scale < __builtin_inff()))
-            word = quantize_pack8(v, st);
-          tile[ts][seg][row] = word;
-          if (seg == 0) {
-            st_s[ts][row] = scale_bits(st.scale);
-            st_z[ts][row] = zero_bits(st.zero);
-          }
-        }
-      } else {
-#pragma unroll
-        for (int i = 0; i < B; ++i) {
-          const int row = sub * RW + (b0 + i) * RPI + rsub;
-          float v[8];
-          unpack_row8<DT>(raw[i], v);
-          float mx = v[0], mn = v[0];
-#pragma unroll
-          for (int j = 1; j < 8; ++j) {
-            mx = max_nan(mx, v[j]);
-            mn = min_nan(mn, v[j]);
-          }
-#pragma unroll
-          for (int off = L / 2; off > 0; off >>= 1) {
-            mx = max_nan(mx, __shfl_xor(mx, off, 64));
-            mn = min_nan(mn, __shfl_xor(mn, off, 64));
-          }
-          const QStats st = group_stats(mx, mn);
-          tile[ts][seg][row] = quantize_pack8(v, st);
-          if (seg == 0) {
-            st_s[ts][row] = scale_bits(st.scale);
-            st_z[ts][row] = zero_bits(st.zero);
-          }
+        group_minmax<L>(mx, mn);
+        float rcp;
+        const QStats st = group_stats_fast(mx, mn, &rcp);
+        bool near;
+        uint32_t word = quantize_pack8_fast(v, st, rcp, &near);
+        // a NaN in the group, a word near a rounding boundary, an infinite
+        // scale (infinite weight) or a scale rounded to 0 in fp16: exact path
+        if (!(mx == mx && mn == mn) || near || !(st.scale > 0.0f && st.scale < __builtin_inff()))
+          word = quantize_pack8(v, st);
+        tile[ts][seg][row] = word;
+        if (seg == 0) {
+          st_s[ts][row] = scale_bits(st.scale);
+          st_z[ts][row] = zero_bits(st.zero);
         }
       }
     }

@@ -156,3 +156,27 @@ def test_quantize_rounding_boundaries(dt, g):
     np.testing.assert_array_equal(qw, rq)
     np.testing.assert_array_equal(s, rs)
     np.testing.assert_array_equal(z, rz)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("g", [8, 16, 32, 64, 128, 256, 512, 1024, -1])
+def test_quantize_degenerate_groups_every_width(dt, g):
+    """NaN, +-inf, zero / underflowing / overflowing scales, ties and signed
+    zeros at every group width (every lane-reduction width of the kernels),
+    interleaved with ordinary rows: bit-exact against the oracle."""
+    from golden.make_golden import degenerate_rows_f32, f32_to_bf16_bits
+
+    K = 2 * g if g > 0 else 512
+    rng = np.random.default_rng(100 + max(g, 0))
+    deg = degenerate_rows_f32(K, g if g > 0 else K // 2, rng)  # (the generator places patterns per half row)
+    ordinary = (rng.standard_normal((deg.shape[0], K)) * 0.02).astype(np.float32)
+    w = np.empty((2 * deg.shape[0] + 1, K), np.float32)
+    w[0:-1:2], w[1:-1:2], w[-1] = deg, ordinary, deg[4]  # odd N: a partial column strip
+    with np.errstate(over="ignore"):  # the 1e30 row overflows fp16 on purpose
+        bits = f32_to_bf16_bits(w) if dt == "bf16" else w.astype(np.float16).view(np.uint16)
+    print(f"[quantize degenerate] G={g} {dt} {w.shape}", flush=True)
+    qw, s, z = _quantize_np(_to_dev(bits, dt), g)
+    rq, rs, rz = O.quantize_int4(bits, dt, g)
+    np.testing.assert_array_equal(qw, rq)
+    np.testing.assert_array_equal(s, rs)
+    np.testing.assert_array_equal(z, rz)
