@@ -699,8 +699,11 @@ Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K) {
         const int64_t S = (KT + T - 1) / T;
         if (S != s || (s > 1 && T < 4)) continue;
         const int64_t wgs = tm * tn * S;
-        const double per_simd = (double)(wgs * nw) / (4.0 * cus);
+        // waves per SIMD on the busiest CU: a fractional round (e.g. 1.5
+        // workgroups per CU) costs the CUs that hold two as much as a full one
+        const double per_simd = (double)((wgs + cus - 1) / cus * nw) / 4.0;
         double t = (double)T * step * (per_simd <= 1.0 ? 1.0 : 0.9 * per_simd);
+        if (nw == 2) t *= 1.3;  // 128-column tiles: each activation tile feeds half the MFMAs
         if (nw == 4 && wgs < cus) t *= 1.07;
         t += 3e-6;
         if (S > 1) {
