@@ -682,7 +682,9 @@ struct Pf2Plan {
 // prologue and epilogue latency plus its output bytes at 5 TB/s; split-K
 // writes fp32 partials instead and adds the reduce kernel (2.2 us plus the
 // partials read at 8 TB/s).
-Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K) {
+// Best plan with at most max_splits K splits; *t_est (if given) receives the
+// model's time for it, in seconds.
+Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K, int max_splits = 8, double* t_est = nullptr) {
   const int cus = device_cu_count();
   const int64_t KT = (K + w4::PF2_BK - 1) / w4::PF2_BK;
   Pf2Plan best;
@@ -695,6 +697,7 @@ Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K) {
     for (int nw : {4, 2}) {
       const int64_t tn = (N + 64 * nw - 1) / (64 * nw);
       for (int s : {1, 2, 4, 8}) {
+        if (s > max_splits) continue;
         const int64_t T = (KT + s - 1) / s;
         const int64_t S = (KT + T - 1) / T;
         if (S != s || (s > 1 && T < 4)) continue;
@@ -725,6 +728,7 @@ Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K) {
       }
     }
   }
+  if (t_est != nullptr) *t_est = best_t;
   return best;
 }
 
@@ -898,8 +902,16 @@ int w4_prefill_grouped_launch(const w4a16_problem* problems, int count, int x_dt
       return W4_ERR_UNSUPPORTED;
     Nt += q.N;
   }
-  const Pf2Plan p = plan_pf2(M, Nt, K);
-  if (p.splits != 1) return W4_ERR_UNSUPPORTED;
+  // one launch without split-K (the tiles of all problems side by side) when
+  // the model puts it below the separate launches with their own plans
+  double t_grouped = 0.0, t_separate = 0.0;
+  const Pf2Plan p = plan_pf2(M, Nt, K, 1, &t_grouped);
+  for (int i = 0; i < count; ++i) {
+    double ti = 0.0;
+    plan_pf2(M, problems[i].N, K, 8, &ti);
+    t_separate += ti;
+  }
+  if (!(t_grouped <= t_separate)) return W4_ERR_UNSUPPORTED;
   w4::Pf3Grouped g{};
   const int64_t bm = 32 * p.mb;
   const int64_t tm = (M + bm - 1) / bm;
