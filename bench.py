@@ -397,7 +397,20 @@ def main() -> int:
                                "gbps": round(block_bytes(M, g) / (msm * 1e-3) / 1e9, 1)}
                 if g == G and M == 16:
                     ms16 = msm
-                del gm, xsm
+                del gm
+                if g == G:
+                    # the block as a model issues it: q/k/v and gate/up share an input
+                    gf = graph_of(lambda: [f for i in range(nsets) for f in (
+                        int4_hip.w4a16_matmul_grouped([xsm[0]] * 3, packs[i][0:3]),
+                        int4_hip.w4a16_matmul(xsm[3], *packs[i][3]),
+                        int4_hip.w4a16_matmul_grouped([xsm[4]] * 2, packs[i][4:6]),
+                        int4_hip.w4a16_matmul(xsm[6], *packs[i][6]))], stream)
+                    time_graph(gf, 2, stream)
+                    msf = time_graph(gf, 5, stream) / nsets
+                    small[g][M]["fused_qkv_gateup_us_per_block"] = round(msf * 1e3, 2)
+                    small[g][M]["fused_qkv_gateup_gbps"] = round(block_bytes(M, g) / (msf * 1e-3) / 1e9, 1)
+                    del gf
+                del xsm
             if g != G:
                 del packs
             torch.cuda.empty_cache()

@@ -711,7 +711,7 @@ Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K, int max_splits = 8, double* t_
         t += 3e-6;
         if (S > 1) {
           const double part = (double)S * M * N * 4;
-          t += part / 5e12 + 2.2e-6 + part / 8e12;
+          t += part / 5e12 + 3.0e-6 + part / 8e12;  // partials written, reduce launch, read back
         } else {
           t += (double)M * N * 2 / 5e12;
         }
