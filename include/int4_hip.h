@@ -145,9 +145,11 @@ size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, i
  *   fp32 partials are summed, in split order, by the last workgroup of each
  *   column tile to finish (in `workspace`).
  *   M > 16: problems that share one activation matrix (same x pointer, K and
- *   group size; at most 4) run as ONE launch of the prefill kernel when its
- *   plan for the concatenated width needs no split-K; otherwise each problem
- *   is one w4a16_gemm call, in order, on `stream` (sharing `workspace`).
+ *   group size; at most 4) run as ONE launch of the prefill kernel (no
+ *   split-K, the tiles of all problems side by side) when the library's
+ *   static cost model puts it below the separate launches; otherwise each
+ *   problem is one w4a16_gemm call, in order, on `stream` (sharing
+ *   `workspace`).  The choice is a pure function of the shapes.
  * `workspace`: 256-byte aligned, w4a16_grouped_workspace_bytes long, laid out
  * like w4a16_gemm's.  Reusing one workspace for calls that run concurrently
  * (on different streams) is a race.  Results are bit-identical run to run.

@@ -1,12 +1,14 @@
 """Y = X @ W_hat^T with X in bf16/fp16 and W given as packed int4 (W4A16), on gfx950.
 
-Same public entry point, launch regimes and error behaviour as the reference
-(int4_triton/gemm.py:223-317):
+Same public entry point, regime boundaries and error behaviour as the
+reference (int4_triton/gemm.py:223-317):
 
-  * M == 1:        decode GEMV, one launch (long K split over workgroups and
-                   finished in-kernel by the last one, in split order);
-  * 2 <= M <= 64:  split-K with fp32 partials and a fixed-order reduce kernel;
-  * M > 64:        tiled MFMA GEMM writing the output dtype directly.
+  * M <= 16:       decode kernel, one launch, no workspace (group sizes >= 32
+                   and dense rows; else split-K with a fixed-order reduce);
+  * 17 <= M <= 64: split-K with fp32 partials and a fixed-order reduce kernel;
+  * M > 64:        tiled MFMA GEMM writing the output dtype directly, split
+                   over K (same partials and reduce) for shapes with too few
+                   output tiles to fill the chip.
 
 The kernels are hand-written HIP (itmo-final-project_amd/csrc); the split
 counts come from a static table inside the library, so results are
