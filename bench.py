@@ -129,17 +129,21 @@ def cpu_baseline(packed, xs_bits, sample_passes: int) -> dict:
 
     from oracle import w4a16_oracle as O
 
-    ts = []
+    ts, per = [], [[] for _ in packed]
     for _ in range(sample_passes):
         t0 = time.perf_counter()
-        for (qw, s, z), xb in zip(packed, xs_bits):
+        for j, ((qw, s, z), xb) in enumerate(zip(packed, xs_bits)):
+            t1 = time.perf_counter()
             O.w4a16_matmul(xb, "bf16", qw, s, z, accumulate="f32")
+            per[j].append(time.perf_counter() - t1)
         ts.append(time.perf_counter() - t0)
     t = float(np.median(ts))
     return {"value": round(block_bytes(1) / t / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"numpy oracle, dequantize(bf16)+matmul over the 7-linear block at M=1, G=128, "
                       f"median of {sample_passes} passes ({t * 1e3:.1f} ms per block)",
-            "ms_per_block": round(t * 1e3, 3)}
+            "ms_per_block": round(t * 1e3, 3),
+            # the single 2048 x 2048 linear is q_proj's shape
+            "per_linear_ms": {name: round(float(np.median(p)) * 1e3, 3) for (name, _, _), p in zip(LINEARS, per)}}
 
 
 def cpu_quantize_baseline(w_bits, q_bytes: int, passes: int) -> dict:
