@@ -351,17 +351,22 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
         }
         xs = Mfma<DT>::m16(xa, ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs);
       }
-      // QS * sum x (q - z) = acc - OFF xs - z (QS xs); tot accumulates s times it
+      // QS * sum x (q - z) = acc - (OFF + QS z) xs, one fma per accumulator
+      // (OFF + QS z is exact for the integer zero points of the format);
+      // tot accumulates s times it
+      float zc[VEC], sc[VEC];
 #pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float ox = Num::OFF * xs[r];
-        const float qx = Num::QS * xs[r];
+      for (int j = 0; j < VEC; ++j) {
+        zc[j] = __builtin_fmaf(Num::QS, ch.z[p].get(j), Num::OFF);
+        sc[j] = ch.s[p].get(j);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-          const float u = __builtin_fmaf(-ch.z[p].get(j), qx, acc[j][r] - ox);
-          tot[j][r] = __builtin_fmaf(ch.s[p].get(j), u, tot[j][r]);
+          const float u = __builtin_fmaf(-zc[j], xs[r], acc[j][r]);
+          tot[j][r] = __builtin_fmaf(sc[j], u, tot[j][r]);
         }
-      }
     }
     __builtin_amdgcn_wave_barrier();  // slots are rewritten by the next chunk
   };
