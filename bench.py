@@ -187,6 +187,55 @@ def device_copy_gbps(dev, stream, nbytes: int = 1 << 30, reps: int = 10) -> floa
     return 2 * nbytes / (ms * 1e-3) / 1e9
 
 
+def hbm_read_ceiling(dev, stream, block_bytes_: int, nsets: int) -> dict | None:
+    """Measured read ceilings (csrc/bench/read_probe.hip, a kernel that only
+    reads): one long stream over 1 GiB, and one launch per set over `nsets`
+    rotated buffers of the decode block's size, replayed from a graph -- the
+    practical bound for a single launch that moves the block's bytes."""
+    import ctypes
+
+    import torch
+
+    path = ROOT / "itmo-final-project_amd" / "int4_hip" / "libw4_bench.so"
+    if not path.exists():
+        log(f"{path} not built; no read ceiling")
+        return None
+    lib = ctypes.CDLL(str(path))
+    fn = lib.w4bench_read
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    sink = torch.zeros(16, dtype=torch.int32, device=dev)
+    raw = stream.cuda_stream
+
+    def launch(buf, nbytes, grid, block):
+        rc = fn(buf.data_ptr(), nbytes, grid, block, sink.data_ptr(), raw)
+        if rc != 0:
+            raise RuntimeError(f"w4bench_read failed ({rc})")
+
+    big = torch.ones(1 << 28, dtype=torch.int32, device=dev)  # 1 GiB
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        for _ in range(2):
+            launch(big, big.numel() * 4, 2048, 256)
+        e0.record(stream)
+        for _ in range(10):
+            launch(big, big.numel() * 4, 2048, 256)
+        e1.record(stream)
+    e1.synchronize()
+    stream_gbps = 10 * big.numel() * 4 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del big
+    n16 = block_bytes_ // 16 * 16
+    bufs = [torch.ones(n16 // 4, dtype=torch.int32, device=dev) for _ in range(nsets)]
+    g = graph_of(lambda: [launch(b, n16, 512, 1024) for b in bufs], stream)
+    time_graph(g, 3, stream)
+    us = time_graph(g, 10, stream) / nsets * 1e3
+    del g, bufs
+    return {"stream_1gib_gbps": round(stream_gbps, 1), "single_launch_block_bytes_us": round(us, 3),
+            "single_launch_block_bytes_gbps": round(n16 / (us * 1e-6) / 1e9, 1),
+            "note": "read-only kernel, 16-byte loads; stream: 2048 x 256 threads over 1 GiB; single launch: "
+                    f"512 x 1024 threads over {n16} B, {nsets} rotated buffers, graph replay"}
+
+
 PROFILE = ROOT / "profiles" / "dec_kernel_one_decode_block_m1.md"
 ROOFLINE_KERNEL = "dec_kernel_one<0, 2>"
 
@@ -486,6 +535,7 @@ def main() -> int:
         if "quantize" in only:
             cpu_q = cpu_quantize_baseline([bits(w) for w in w16_host], q_bytes, 3)
     copy_gbps = device_copy_gbps(dev, stream) if "decode" in only else None
+    read_ceiling = hbm_read_ceiling(dev, stream, bytes1, nsets) if "decode" in only else None
 
     traffic = profiled_traffic()
     out = {
@@ -531,6 +581,7 @@ def main() -> int:
         "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None,
         "cpu_baseline_quantize": cpu_q,
         "hbm_device_copy_gbps": round(copy_gbps, 1) if copy_gbps else None,
+        "hbm_read_ceiling": read_ceiling,
         "llama_1b_w4": llama,
         "device": torch.cuda.get_device_name(dev),
     }

@@ -21,6 +21,9 @@ ROOT = HERE.parent
 CSRC = HERE / "csrc"
 BUILD = HERE / "_build"
 LIB = HERE / "int4_hip" / "libint4_hip.so"
+# measurement helpers for bench.py (not part of the library)
+BENCH_SRC = CSRC / "bench"
+BENCH_LIB = HERE / "int4_hip" / "libw4_bench.so"
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -47,7 +50,7 @@ def sources() -> list[Path]:
 
 
 def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
+    obj = BUILD / ((src.parent.name + "_" if src.parent == BENCH_SRC else "") + src.stem + ".o")
     cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
     if src.suffix == ".cpp":
         cmd = [hipcc(), "-O3", "-std=c++17", "-fPIC", "-I", str(ROOT / "include"), "-I", str(CSRC),
@@ -71,8 +74,17 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stderr}")
     os.replace(tmp, LIB)
+    bench_srcs = sorted(BENCH_SRC.glob("*.hip"))
+    if bench_srcs:
+        bobjs = [_compile(s) for s in bench_srcs]
+        btmp = BENCH_LIB.with_suffix(".so.tmp")
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(btmp), *map(str, bobjs)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stderr}")
+        os.replace(btmp, BENCH_LIB)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources", file=sys.stderr)
+        print(f"built {LIB} from {len(srcs)} sources (+ {BENCH_LIB.name})", file=sys.stderr)
     return LIB
 
 
