@@ -257,6 +257,15 @@ def summarize_prof(d: Path, kernel: str = ROOFLINE_KERNEL) -> str:
                 if match(r["Kernel_Name"]) and r["Counter_Name"] == name]
         return sum(vals) / len(vals) if vals else None
 
+    def first_dispatch(sub, name, match):
+        # the calibration copy is the run's first device copy (later copies,
+        # e.g. the 1 GiB copy-rate measurement, move other sizes)
+        rs = [r for r in rows(sub, "counter_collection") if match(r["Kernel_Name"]) and r["Counter_Name"] == name]
+        if not rs:
+            return None
+        first = min(int(r["Dispatch_Id"]) for r in rs)
+        return sum(float(r["Counter_Value"]) for r in rs if int(r["Dispatch_Id"]) == first)
+
     out = []
     stats = [r for r in rows("trace", "kernel_stats") if kernel in r["Name"]]
     dur_ns = float(stats[0]["AverageNs"]) if stats else None
@@ -266,7 +275,7 @@ def summarize_prof(d: Path, kernel: str = ROOFLINE_KERNEL) -> str:
                    f"min {float(r['MinNs']) / 1e3:.3f} us, max {float(r['MaxNs']) / 1e3:.3f} us")
     is_copy = lambda n: "copyBuffer" in n  # noqa: E731
     is_k = lambda n: kernel in n  # noqa: E731
-    f_copy, w_copy = counter("fetch", "FETCH_SIZE", is_copy), counter("write", "WRITE_SIZE", is_copy)
+    f_copy, w_copy = first_dispatch("fetch", "FETCH_SIZE", is_copy), first_dispatch("write", "WRITE_SIZE", is_copy)
     f_k, w_k = counter("fetch", "FETCH_SIZE", is_k), counter("write", "WRITE_SIZE", is_k)
     traffic = None
     if None not in (f_copy, w_copy, f_k, w_k):
