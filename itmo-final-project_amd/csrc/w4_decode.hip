@@ -78,7 +78,9 @@ constexpr int kDecBufFlags = 0x00020000;   // raw buffer, 32-bit data format
 // 256 MB Infinity Cache holds (a Llama-3.2-1B token reads 517 MB), and
 // streaming them with nt took the rotated-weights M = 1 block from 10.2 to
 // 9.6 us.  A weight set small enough to stay cache-resident between calls
-// loses that reuse (6.2 -> 8.2 us per block in that case).
+// loses that reuse (6.2 -> 8.2 us per block in that case).  Scales and zeros
+// are read once per call as well and take the same policy (M = 1 block
+// 9.5 -> 9.2 us with both).
 constexpr int kDecWeightAux = 2;
 
 template <int DT>
@@ -535,8 +537,8 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     r.x = __builtin_amdgcn_raw_buffer_load_b128(rx, (((uint32_t)sb * RPS + (uint32_t)lane) * 16u) | x_oob | oob, 0, 0);
     const uint32_t g0 = (uint32_t)((sb * SK) >> a.gshift);
     const uint32_t so = (g0 * (uint32_t)N * 2u + sz_lane) | sz_oob | oob;
-    r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, 0);
-    r.z = __builtin_amdgcn_raw_buffer_load_b128(rz, so, 0, 0);
+    r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, kDecWeightAux);
+    r.z = __builtin_amdgcn_raw_buffer_load_b128(rz, so, 0, kDecWeightAux);
     __builtin_amdgcn_sched_barrier(0);
     const uint32_t vo = ((uint32_t)sb * step_bytes + w_lane) | oob;
 #pragma unroll
@@ -615,12 +617,23 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   if (tid < TW) {
     const int n = n0 + tid;
     if (n < N) {
-      float v = 0.0f;
+      // every partial is read before the first add (one LDS latency instead
+      // of one per few reads); the adds keep the wave order
+      constexpr int NPART = TW == 32 ? 2 * kOneWaves : kOneWaves;
+      float pv[NPART];
 #pragma unroll
       for (int w = 0; w < kOneWaves; ++w) {
-        v += red[w * 128 + tid];
-        if constexpr (TW == 32) v += red[w * 128 + 32 + tid];
+        if constexpr (TW == 32) {
+          pv[2 * w] = red[w * 128 + tid];
+          pv[2 * w + 1] = red[w * 128 + 32 + tid];
+        } else {
+          pv[w] = red[w * 128 + tid];
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
+      float v = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NPART; ++i) v += pv[i];
       a.y[n] = float_to_act_bits<DT>(v * (1.0f / Num::QS));
     }
   }
