@@ -409,9 +409,20 @@ __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
 }
 
-template <int DT, int NW, bool SZK, int MB>
+// KH = 2: the workgroup holds two sets of NW waves that run the same tile
+// over the two halves of its K range, each with its own LDS ring, in
+// lockstep (one barrier per step for all of them); the second set's
+// accumulators are added to the first set's through LDS at the end, in that
+// fixed order.  This puts two waves on every SIMD for tiles that would
+// otherwise leave one wave per SIMD, without writing split-K partials.  The
+// host uses it for 32-row tiles only: there it measured 5-7 % faster (the
+// grouped q/k/v and gate/up launches at M = 128); with 64- and 128-row tiles
+// the lockstep halves ran no faster than one wave per SIMD, or slower
+// (down_proj at M = 2048: 71 against 68 us).
+template <int DT, int NW, bool SZK, int MB, int KH>
 __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   typedef typename Act<DT>::frag F;
+  static_assert(KH == 1 || KH == 2, "K halves");
   constexpr int BM = 32 * MB;        // rows per tile: MB blocks of 32
   constexpr int XL = BM / 8 / NW;    // direct-to-LDS activation loads per wave per step (1 KB each)
   static_assert(XL >= 1, "activation loads per wave");
@@ -421,11 +432,14 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   constexpr int WAIT_IMM = (WAITN & 15) | 0x70 | 0xF00 | ((WAITN >> 4) << 14);
   constexpr int SLOT = BM * PF2_BK;  // elements of one LDS slot
   static_assert(WAITN < 64, "vmcnt range");
-  __shared__ __attribute__((aligned(16))) uint16_t xs[4 * SLOT];
+  __shared__ __attribute__((aligned(16))) uint16_t xs_all[KH * 4 * SLOT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int kh = KH == 1 ? 0 : wave / NW;  // K half of this wave
+  const int wn = wave - kh * NW;
+  uint16_t* const xs = xs_all + kh * 4 * SLOT;
   const int l32 = lane & 31, lh = lane >> 5;
   const int split = t / a.tiles_mn;
   const int tmn = t - split * a.tiles_mn;
@@ -435,8 +449,10 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   const int n0w = (tile_n * NW + wn) * 64;
   const int N = a.N;
   const int KT = a.K / PF2_BK;
-  const int kt0 = split * a.kt_per_split;
-  const int nsteps = min(a.kt_per_split, KT - kt0);
+  // KH = 2: the host gives every split the same even number of steps, so both
+  // halves run the same number of steps (and barriers)
+  const int kt0 = split * a.kt_per_split + kh * (a.kt_per_split / KH);
+  const int nsteps = KH == 1 ? min(a.kt_per_split, KT - kt0) : a.kt_per_split / KH;
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, 0x00020000);
@@ -578,27 +594,55 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   if (st + 1 < nsteps) step(r1, r2, st + 1);
   __builtin_amdgcn_s_waitcnt(0);  // no load (and no LDS write) outstanding past the loop
 
+  if constexpr (KH == 2) {
+    // second half's accumulators -> LDS (lane-major, conflict-free) -> added
+    // to the first half's; NW waves x MB * 2 * 16 * 64 floats fill the two rings
+    constexpr int PER = MB * 2 * 16 * 64;
+    static_assert(NW * PER * 4 <= KH * 4 * SLOT * 2, "partials fit the rings");
+    float* const P = reinterpret_cast<float*>(xs_all) + wn * PER;
+    __syncthreads();  // every wave is past its last ring read
+    if (kh == 1) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) P[((mb * 2 + nb) * 16 + r) * 64 + lane] = acc[mb][nb][r];
+    }
+    __syncthreads();
+    if (kh == 0) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mb][nb][r] += P[((mb * 2 + nb) * 16 + r) * 64 + lane];
+    }
+  }
+
   constexpr int TW = 64 * NW;  // tile width (elements)
   if (BM * TW <= 4 * SLOT && a.ws == nullptr && a.y16) {
     // Output through LDS: the tile (BM x 64 NW values of the output dtype,
     // when it fits the four ring slots) is assembled there, then written back
     // as 16-byte chunks, whole 64 NW-wide row segments per 64 NW / 8 lanes
     // instead of 128-byte pieces per lane pair.
-    __syncthreads();  // every wave is past its last A-fragment read
-    uint32_t* T = reinterpret_cast<uint32_t*>(xs);
+    __syncthreads();  // every wave is past its last A-fragment (or partial) read
+    uint32_t* T = reinterpret_cast<uint32_t*>(xs_all);
+    if (kh == 0) {
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = mb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-        T[row * (TW / 2) + wn * 32 + l32] = (uint32_t)float_to_act_bits<DT>(acc[mb][0][r]) |
-                                            ((uint32_t)float_to_act_bits<DT>(acc[mb][1][r]) << 16);
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int row = mb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+          T[row * (TW / 2) + wn * 32 + l32] = (uint32_t)float_to_act_bits<DT>(acc[mb][0][r]) |
+                                              ((uint32_t)float_to_act_bits<DT>(acc[mb][1][r]) << 16);
+        }
+    }
     __syncthreads();
     constexpr int CPR = TW / 8;  // 16-byte chunks per tile row
     const int n0 = tile_n * TW;
 #pragma unroll 4
-    for (int c = tid; c < BM * CPR; c += NW * 64) {
+    for (int c = tid; c < BM * CPR; c += NW * KH * 64) {
       const int row = c / CPR, cc = c - row * CPR;
       const int m = m0 + row, n = n0 + cc * 8;
       if (m < a.M && n < N)
@@ -611,7 +655,7 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   }
 
   const int n = n0w + 2 * l32;
-  if (n < N) {
+  if (kh == 0 && n < N) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -633,9 +677,9 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
 }
 
 
-template <int DT, int NW, bool SZK, int MB>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_kernel(Pf2Args a) {
-  pf3_tile<DT, NW, SZK, MB>(a, (int)blockIdx.x);
+template <int DT, int NW, bool SZK, int MB, int KH>
+__global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_kernel(Pf2Args a) {
+  pf3_tile<DT, NW, SZK, MB, KH>(a, (int)blockIdx.x);
 }
 
 // Several products sharing one activation matrix (q/k/v, gate/up) in one
@@ -647,14 +691,14 @@ struct Pf3Grouped {
   int count;
 };
 
-template <int DT, int NW, bool SZK, int MB>
-__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_grouped_kernel(Pf3Grouped g) {
+template <int DT, int NW, bool SZK, int MB, int KH>
+__global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_grouped_kernel(Pf3Grouped g) {
   const int b = (int)blockIdx.x;
   int p = 0;
 #pragma unroll
   for (int i = 1; i < PF3_MAX_GROUPED; ++i)
     if (i < g.count && b >= g.wg_start[i]) p = i;
-  pf3_tile<DT, NW, SZK, MB>(g.prob[p], b - g.wg_start[p]);
+  pf3_tile<DT, NW, SZK, MB, KH>(g.prob[p], b - g.wg_start[p]);
 }
 }  // namespace w4
 
@@ -663,7 +707,7 @@ using namespace w4host;
 namespace {
 
 struct Pf2Plan {
-  int nw = 0, mb = 4, splits = 1, kt_per_split = 0, tiles_n = 0, tiles_mn = 0;
+  int nw = 0, mb = 4, kh = 1, splits = 1, kt_per_split = 0, tiles_n = 0, tiles_mn = 0;
   size_t ws = 0;
 };
 
@@ -695,13 +739,20 @@ Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K, int max_splits = 8, double* t_
         const int64_t T = (KT + s - 1) / s;
         const int64_t S = (KT + T - 1) / T;
         if (S != s || (s > 1 && T < 4)) continue;
+        for (int kh : {1, 2}) {
+        // two K halves per workgroup: 32-row tiles and four-wave sets only,
+        // every split the same even number of steps (both halves run in
+        // lockstep)
+        if (kh == 2 && (mb != 1 || nw != 4 || K % w4::PF2_BK != 0 || T % 2 != 0 || S * T != KT || T < 8))
+          continue;
         const int64_t wgs = tm * tn * S;
         // waves per SIMD on the busiest CU: a fractional round (e.g. 1.5
         // workgroups per CU) costs the CUs that hold two as much as a full one
-        const double per_simd = (double)((wgs + cus - 1) / cus * nw) / 4.0;
-        double t = (double)T * step * (per_simd <= 1.0 ? 1.0 : 0.9 * per_simd);
+        const double per_simd = (double)((wgs + cus - 1) / cus * nw * kh) / 4.0;
+        double t = (double)(T / kh) * step * (per_simd <= 1.0 ? 1.0 : 0.9 * per_simd);
         if (nw == 2) t *= 1.3;  // 128-column tiles: each activation tile feeds half the MFMAs
         if (nw == 4 && wgs < cus) t *= 1.07;
+        if (kh == 2) t += 0.7e-6;  // the halves' sum through LDS
         t += 3e-6;
         if (S > 1) {
           const double part = (double)S * M * N * 4;
@@ -713,11 +764,13 @@ Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K, int max_splits = 8, double* t_
           best_t = t;
           best.nw = nw;
           best.mb = mb;
+          best.kh = kh;
           best.splits = (int)S;
           best.kt_per_split = (int)T;
           best.tiles_n = (int)tn;
           best.tiles_mn = (int)(tm * tn);
           best.ws = S > 1 ? (size_t)S * M * N * sizeof(float) : 0;
+        }
         }
       }
     }
@@ -733,13 +786,24 @@ bool pf2_ok(const void* x, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t
          M < (1LL << 30) && ((M - 1) * sxm + K) * 2 < (1LL << 31) && (K / 8) * N * 4 < (1LL << 31);
 }
 
+template <int DT, int NW, int MB, int KH>
+void pf3_launch_k(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t st) {
+  const dim3 grid((unsigned)(p.tiles_mn * p.splits)), block(NW * KH * 64);
+  if (szk)
+    hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, true, MB, KH>), grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, false, MB, KH>), grid, block, 0, st, a);
+}
+
 template <int DT, int NW, int MB>
 void pf3_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t st) {
-  const dim3 grid((unsigned)(p.tiles_mn * p.splits)), block(NW * 64);
-  if (szk)
-    hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, true, MB>), grid, block, 0, st, a);
-  else
-    hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, false, MB>), grid, block, 0, st, a);
+  if constexpr (NW == 4 && MB == 1) {
+    if (p.kh == 2) {
+      pf3_launch_k<DT, NW, MB, 2>(p, szk, a, st);
+      return;
+    }
+  }
+  pf3_launch_k<DT, NW, MB, 1>(p, szk, a, st);
 }
 
 template <int DT, int NW>
@@ -854,18 +918,20 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
 
 namespace {
 
-template <int DT, int NW, int MB>
+template <int DT, int NW, int MB, int KH = 1>
 void pf3_grouped_go(bool szk, const w4::Pf3Grouped& g, int wgs, hipStream_t st) {
-  const dim3 grid((unsigned)wgs), block(NW * 64);
+  const dim3 grid((unsigned)wgs), block(NW * KH * 64);
   if (szk)
-    hipLaunchKernelGGL((w4::pf3_grouped_kernel<DT, NW, true, MB>), grid, block, 0, st, g);
+    hipLaunchKernelGGL((w4::pf3_grouped_kernel<DT, NW, true, MB, KH>), grid, block, 0, st, g);
   else
-    hipLaunchKernelGGL((w4::pf3_grouped_kernel<DT, NW, false, MB>), grid, block, 0, st, g);
+    hipLaunchKernelGGL((w4::pf3_grouped_kernel<DT, NW, false, MB, KH>), grid, block, 0, st, g);
 }
 
 template <int DT>
 void pf3_grouped_dt(const Pf2Plan& p, bool szk, const w4::Pf3Grouped& g, int wgs, hipStream_t st) {
-  if (p.nw == 4) {
+  if (p.nw == 4 && p.mb == 1 && p.kh == 2) {
+    pf3_grouped_go<DT, 4, 1, 2>(szk, g, wgs, st);
+  } else if (p.nw == 4) {
     if (p.mb == 4) pf3_grouped_go<DT, 4, 4>(szk, g, wgs, st);
     else if (p.mb == 2) pf3_grouped_go<DT, 4, 2>(szk, g, wgs, st);
     else pf3_grouped_go<DT, 4, 1>(szk, g, wgs, st);

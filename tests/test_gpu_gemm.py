@@ -260,6 +260,18 @@ def test_prefill_group_sizes_and_partial_tiles(M, G, NK):
     _check(out, x, qw, s, z)
 
 
+# shapes whose static plan runs 32-row tiles as workgroups of two K halves
+# (eight waves, the halves summed through LDS)
+@pytest.mark.parametrize("M,N,K", [(256, 8192, 2048), (1024, 2048, 2048)])
+def test_prefill_two_k_halves(M, N, K):
+    print(f"[prefill-kh] M={M} N={N} K={K}", flush=True)
+    qw, s, z = _weights(N, K, 128, seed=M + 7)
+    x = randn((M, K), seed=M + 8).to(DEV)
+    out = int4_hip.w4a16_matmul(x, qw, s, z)
+    _check(out, x, qw, s, z)
+    assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
+
+
 @pytest.mark.parametrize("M", [128, 512])
 @pytest.mark.parametrize("NK", [(512, 2048), (2048, 8192)])
 def test_prefill_split_k_bit_identical(M, NK):
@@ -279,7 +291,8 @@ def test_prefill_split_k_bit_identical(M, NK):
 # oracle, repeat calls bit-identical
 @pytest.mark.parametrize("G", [32, 128])
 @pytest.mark.parametrize("M,K,Ns", [(130, 512, (256, 64, 64)), (300, 256, (1024, 256, 256)),
-                                     (512, 512, (192, 72, 120)), (40, 512, (128, 64))])
+                                     (512, 512, (192, 72, 120)), (40, 512, (128, 64)),
+                                     (128, 2048, (2048, 512, 512))])
 def test_grouped_shared_activation(M, K, Ns, G):
     print(f"[grouped-prefill] M={M} K={K} Ns={Ns} G={G}", flush=True)
     ws = [_weights(N, K, G, seed=400 + i) for i, N in enumerate(Ns)]
