@@ -409,7 +409,7 @@ def main() -> int:
     def single(i, j):
         return lambda: int4_hip.w4a16_matmul(xs1[i][j], *packed[i][j])
 
-    per_lin, ms7, resident = {}, None, None
+    per_lin, ms7, ms4, resident = {}, None, None, None
     if "perlinear" in only:
         for j, (name, N, K) in enumerate(LINEARS):
             gj = graph_of(lambda j=j: [single(i, j)() for i in range(nsets)], stream)
@@ -420,6 +420,15 @@ def main() -> int:
         time_graph(g7, 2, stream)
         ms7 = time_graph(g7, 10, stream) / nsets
         del g7
+        # the block as a decoder issues it (4 calls: q/k/v and gate/up share an input)
+        g4 = graph_of(lambda: [f for i in range(nsets) for f in (
+            int4_hip.w4a16_matmul_grouped([xs1[i][0]] * 3, packed[i][0:3]),
+            int4_hip.w4a16_matmul(xs1[i][3], *packed[i][3]),
+            int4_hip.w4a16_matmul_grouped([xs1[i][4]] * 2, packed[i][4:6]),
+            int4_hip.w4a16_matmul(xs1[i][6], *packed[i][6]))], stream)
+        time_graph(g4, 2, stream)
+        ms4 = time_graph(g4, 10, stream) / nsets
+        del g4
         # cache-resident figures (one weight set, 32 MB, replayed: it stays in
         # the 256 MB Infinity Cache), comparable to L2-resident numbers
         gr = graph_of(lambda: [grouped(0)() for _ in range(nsets)], stream)
@@ -460,6 +469,15 @@ def main() -> int:
                 if g == G and M == 16:
                     ms16 = msm
                 del gm
+                if M <= 16:
+                    # all seven products in one launch (as the M=1 headline figure)
+                    gg = graph_of(lambda: [int4_hip.w4a16_matmul_grouped(xsm, packs[i]) for i in range(nsets)],
+                                  stream)
+                    time_graph(gg, 2, stream)
+                    msg = time_graph(gg, 5, stream) / nsets
+                    small[g][M]["grouped_us_per_block"] = round(msg * 1e3, 2)
+                    small[g][M]["grouped_gbps"] = round(block_bytes(M, g) / (msg * 1e-3) / 1e9, 1)
+                    del gg
                 if g == G:
                     # the block as a model issues it: q/k/v and gate/up share an input
                     gf = graph_of(lambda: [f for i in range(nsets) for f in (
@@ -580,6 +598,8 @@ def main() -> int:
             k: round(v, 3) for k, v in resident.items()},
         "decode_m1_7_launches_us_per_block": round(ms7 * 1e3, 3) if ms7 else None,
         "decode_m1_7_launches_gbps": round(bytes1 / (ms7 * 1e-3) / 1e9, 1) if ms7 else None,
+        "decode_m1_4_calls_us_per_block": round(ms4 * 1e3, 3) if ms4 else None,
+        "decode_m1_4_calls_gbps": round(bytes1 / (ms4 * 1e-3) / 1e9, 1) if ms4 else None,
         "small_m_7_launches": {f"G{g}": {f"M{m}": v for m, v in d.items()} for g, d in small.items()},
         "splitk_m16_us_per_block": round(ms16 * 1e3, 3) if ms16 else None,
         "splitk_m16_gbps": round(block_bytes(16) / (ms16 * 1e-3) / 1e9, 1) if ms16 else None,

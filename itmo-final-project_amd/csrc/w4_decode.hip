@@ -821,7 +821,13 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   } else {
     dp.gs = (int)std::min(G / 32, 8);  // dec_kernel: steps per group, capped at 8
     dp.threads = w4::kDecThreads;
-    dp.mx = M <= 4 ? 4 : M <= 8 ? 8 : 16;
+    // rows staged per wave: the smallest width that holds M rows, except that
+    // launches with more workgroups than CUs stage 8 rows for M <= 4 as well
+    // (measured: the 7-linear block in one launch at M = 2 / 4 takes 10.8 /
+    // 10.9 us with 8 rows against 12.2 / 12.4 us with 4, while launches of at
+    // most one workgroup per CU are 6 % slower with 8); the rows fed to the
+    // MFMA, and so every output bit, do not depend on it
+    dp.mx = (M <= 4 && wgs <= device_cu_count()) ? 4 : M <= 8 ? 8 : 16;
     bool narrow = false;  // a tile of vec < 4 has chunks of 8 steps (32 slices per row)
     for (int s = 0; s < count; ++s) narrow = narrow || dp.g.prob[s].vec < 4;
     // ONE: activation slots + reduction; M > 1: activation areas (at most
