@@ -26,7 +26,9 @@
 // are raw buffer loads; a chunk past the end of a wave's run uses an offset
 // that the hardware range check turns into zeros with no memory traffic, so
 // the load sequence is unconditional.  The per-wave partial tiles are summed
-// through LDS in wave order, so every output bit is fixed.
+// through LDS in wave order, so every output bit is fixed.  (M <= 4 with
+// 16-byte aligned weights and N % 8 == 0, K <= 8192: the one-workgroup-per-CU
+// kernel further down, dec_kernel_one, instead.)
 //
 // Nibble order.  The four dwords built from one packed word hold nibbles
 // (0,4), (1,5), (2,6), (3,7); the activation fragment is permuted to the same
@@ -424,7 +426,7 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   }
 }
 
-// ---------------------------------------------------------------- M == 1 path
+// ------------------------------------------ M <= 4 path (one workgroup per CU)
 //
 // One workgroup of 16 waves per CU-sized unit of work: a column tile over the
 // whole K of about 128 KB of packed weights, so that the seven linears of a
@@ -452,13 +454,21 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
 //        reduction.
 // Activations (permuted to the nibble order), scales and zeros are staged in
 // a per-wave LDS area that only the wave itself reads (no barrier).
+//
+// Up to four activation rows (MR = 4, 2 <= M <= 4): A-operand row r carries
+// activation row r % 4 (T128 and T32 keep their two halves, rows 0..3 and
+// 8..11; rows 4..7 and 12..15 repeat them and are ignored), rows past M are
+// staged as zeros, and the accumulator elements 0..3 of the owner lanes hold
+// the rows 0..3 of their columns, each corrected with its own activation sum.
 constexpr int kOneWaves = 16;
 constexpr int kOneThreads = 64 * kOneWaves;
-constexpr int kOneWaveLds = 3072;  // per wave: activations 1 KB, scales 1 KB, zeros 1 KB
-constexpr int kOneRedOffset = kOneWaves * kOneWaveLds;
-constexpr int kOneLds = kOneRedOffset + kOneWaves * 128 * (int)sizeof(float);
+// per wave: activations MR KB, scales 1 KB, zeros 1 KB; then the reduction
+// area, MR x 128 floats per wave
+constexpr int one_wave_lds(int mr) { return mr * 1024 + 2048; }
+constexpr int one_red_offset(int mr) { return kOneWaves * one_wave_lds(mr); }
+constexpr int one_lds(int mr) { return one_red_offset(mr) + kOneWaves * mr * 128 * (int)sizeof(float); }
 
-template <int DT, int TW, int GSI, int NL, int D>
+template <int DT, int TW, int GSI, int NL, int D, int MR>
 __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t* lds) {
   typedef typename Act<DT>::frag F;
   typedef DecNum<DT> Num;
@@ -469,7 +479,11 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   constexpr int GS = GSI < NL ? GSI : NL;                // correction interval (steps)
   constexpr int NP = NL / GS;                            // correction points = staged groups
   constexpr int LPG = TW / 8;                            // lanes per staged group row (16 B)
-  constexpr int XE = NL * RPS;                           // activation entries (8 k) per round
+  constexpr int XE = NL * RPS;                           // activation entries (8 k) per round and row
+  constexpr int XLD = (MR * XE + 63) / 64;               // activation loads per round and lane
+  constexpr int WLDS = one_wave_lds(MR);
+  static_assert(MR == 1 || MR == 4, "activation rows");
+  static_assert(MR == 1 || D == 1, "four rows: single-round tilings only");
   static_assert(XE <= 64 && NP * LPG <= 64 && NL * SLOTS * 16 <= 1024, "per-wave staging area");
   static_assert(GSI >= 1 && (NL % GS) == 0, "correction interval");
 
@@ -477,9 +491,11 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane % QPR, lr = lane / QPR;  // load quad and row within a step
-  // A-operand slot within a step (T128: slots 2 and 3 stay zero)
+  // A-operand slot within a step (T128: slots 2 and 3 stay zero) and the
+  // activation row of this lane's A-operand row
   int a_slot = lr;
   if constexpr (TW == 128) a_slot = (((lane & 15) >> 3) == ((lane >> 4) & 1)) ? (lane >> 5) : 2;
+  const int a_row = MR == 1 ? 0 : (lane & 3);
   // result owners: output quad oq (columns 4 oq .. 4 oq + 3) and part
   bool owner;
   int oq, part = 0;
@@ -494,7 +510,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     oq = lane & 7;
     part = lane >= 40 ? 1 : 0;
   }
-  const int N = a.N, K = a.K;
+  const int N = a.N, K = a.K, M = MR == 1 ? 1 : a.M;
   const int n0 = tile * TW;
   const int S = K / SK;
   const int per_wave = ((S + kOneWaves - 1) / kOneWaves + NL - 1) / NL * NL;
@@ -512,29 +528,40 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
 
   const uint32_t step_bytes = (uint32_t)RPS * 4u * (uint32_t)N;
   const uint32_t w_lane = ((uint32_t)lr * (uint32_t)N + (uint32_t)(n0 + 4 * lq)) * 4u;
-  const uint32_t x_oob = lane < XE ? 0u : kDecOOB;
+  // activation entry f = 64 j + lane of a round: row f / XE, entry f % XE
+  // (k8 row sb * RPS + f % XE); entries of rows past M read zeros
+  uint32_t x_lane[XLD];
+#pragma unroll
+  for (int j = 0; j < XLD; ++j) {
+    const int f = 64 * j + lane, m = f / XE, e = f % XE;
+    x_lane[j] = (f < MR * XE && m < M) ? ((uint32_t)m * (uint32_t)a.sxm + (uint32_t)e * 8u) * 2u : kDecOOB;
+  }
   const uint32_t sz_oob = lane < NP * LPG ? 0u : kDecOOB;
   const uint32_t sz_lane = (uint32_t)(lane / LPG) * (uint32_t)N * 2u + (uint32_t)(n0 * 2 + (lane % LPG) * 16);
-  uint8_t* x_lds = lds + wv * kOneWaveLds;
-  uint8_t* s_lds = x_lds + 1024;
-  uint8_t* z_lds = x_lds + 2048;
+  uint8_t* x_lds = lds + wv * WLDS;
+  uint8_t* s_lds = x_lds + MR * 1024;
+  uint8_t* z_lds = s_lds + 1024;
   const uint32_t magic = dec_magic_vgpr<DT>();
   const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
   if constexpr (TW == 128) {
-    // the zero A slots (2 and 3 of every step) are never rewritten
-    if (lane < 2 * NL)
-      *reinterpret_cast<u32x4*>(x_lds + ((lane >> 1) * SLOTS + 2 + (lane & 1)) * 16) = u32x4{0u, 0u, 0u, 0u};
+    // the zero A slots (2 and 3 of every step and row) are never rewritten
+    if (lane < 2 * NL * MR) {
+      const int m = lane / (2 * NL), e = lane % (2 * NL);
+      *reinterpret_cast<u32x4*>(x_lds + ((m * NL + (e >> 1)) * SLOTS + 2 + (e & 1)) * 16) = u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   struct Round {
     u32x4 w[NL];
-    u32x4 x, s, z;
+    u32x4 x[XLD], s, z;
   };
   // Issue order = order of use: activations, scales, zeros, weights.
   auto load_round = [&](Round& r, int sb) {
     const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
     __builtin_amdgcn_sched_barrier(0);
-    r.x = __builtin_amdgcn_raw_buffer_load_b128(rx, (((uint32_t)sb * RPS + (uint32_t)lane) * 16u) | x_oob | oob, 0, 0);
+#pragma unroll
+    for (int j = 0; j < XLD; ++j)
+      r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (x_lane[j] + (uint32_t)sb * RPS * 16u) | oob, 0, 0);
     const uint32_t g0 = (uint32_t)((sb * SK) >> a.gshift);
     const uint32_t so = (g0 * (uint32_t)N * 2u + sz_lane) | sz_oob | oob;
     r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, kDecWeightAux);
@@ -549,12 +576,20 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
 
   f32x4 acc[4];
   f32x4 xs;
-  float tot[4] = {0.f, 0.f, 0.f, 0.f};
+  float tot[4][MR];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) tot[j][m] = 0.f;
 
   auto compute_round = [&](const Round& r, int sb) {
     // stage the round's activations (permuted), scales and zeros
-    if (lane < XE)
-      *reinterpret_cast<u32x4*>(x_lds + ((lane / RPS) * SLOTS + lane % RPS) * 16) = dec_perm_x(r.x);
+#pragma unroll
+    for (int j = 0; j < XLD; ++j) {
+      const int f = 64 * j + lane, m = f / XE, e = f % XE;
+      if (f < MR * XE)
+        *reinterpret_cast<u32x4*>(x_lds + ((m * NL + e / RPS) * SLOTS + e % RPS) * 16) = dec_perm_x(r.x[j]);
+    }
     *reinterpret_cast<u32x4*>(s_lds + lane * 16) = r.s;
     *reinterpret_cast<u32x4*>(z_lds + lane * 16) = r.z;
     __builtin_amdgcn_wave_barrier();
@@ -563,7 +598,8 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
 #pragma unroll
       for (int i = 0; i < GS; ++i) {
         const int st = p * GS + i;
-        const F xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(x_lds + (st * SLOTS + a_slot) * 16));
+        const F xa = __builtin_bit_cast(
+            F, *reinterpret_cast<const u32x4*>(x_lds + ((a_row * NL + st) * SLOTS + a_slot) * 16));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const F b = __builtin_bit_cast(F, Num::bvals(r.w[st][j], magic));
@@ -575,14 +611,15 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       const int gp = ((sb + p * GS) * SK >> a.gshift) - ((sb * SK) >> a.gshift);
       const u32x2 sv = *reinterpret_cast<const u32x2*>(s_lds + gp * TW * 2 + oq * 8);
       const u32x2 zv = *reinterpret_cast<const u32x2*>(z_lds + gp * TW * 2 + oq * 8);
-      const float ox = Num::OFF * xs[0];
-      const float qx = Num::QS * xs[0];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const float sj = half_bits_to_float((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
         const float zj = half_bits_to_float((uint16_t)(zv[j >> 1] >> (16 * (j & 1))));
-        const float u = __builtin_fmaf(-zj, qx, acc[j][0] - ox);
-        tot[j] = __builtin_fmaf(sj, u, tot[j]);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const float u = __builtin_fmaf(-zj, Num::QS * xs[m], acc[j][m] - Num::OFF * xs[m]);
+          tot[j][m] = __builtin_fmaf(sj, u, tot[j][m]);
+        }
       }
     }
     __builtin_amdgcn_wave_barrier();  // the next round rewrites the staging area
@@ -608,40 +645,44 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   }
 
   // cross-wave (T32: and even/odd row) reduction in a fixed order
-  float* red = reinterpret_cast<float*>(lds + kOneRedOffset);
+  float* red = reinterpret_cast<float*>(lds + one_red_offset(MR));
   if (owner) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) red[wv * 128 + part * 32 + 4 * oq + j] = tot[j];
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) red[(wv * MR + m) * 128 + part * 32 + 4 * oq + j] = tot[j][m];
   }
   __syncthreads();
-  if (tid < TW) {
-    const int n = n0 + tid;
-    if (n < N) {
+  if (tid < MR * TW) {
+    const int m = tid / TW, nl = tid - m * TW;
+    const int n = n0 + nl;
+    if (m < M && n < N) {
       // every partial is read before the first add (one LDS latency instead
       // of one per few reads); the adds keep the wave order
       constexpr int NPART = TW == 32 ? 2 * kOneWaves : kOneWaves;
       float pv[NPART];
 #pragma unroll
       for (int w = 0; w < kOneWaves; ++w) {
+        const float* rw = red + (w * MR + m) * 128;
         if constexpr (TW == 32) {
-          pv[2 * w] = red[w * 128 + tid];
-          pv[2 * w + 1] = red[w * 128 + 32 + tid];
+          pv[2 * w] = rw[nl];
+          pv[2 * w + 1] = rw[32 + nl];
         } else {
-          pv[w] = red[w * 128 + tid];
+          pv[w] = rw[nl];
         }
       }
       __builtin_amdgcn_sched_barrier(0);
       float v = 0.0f;
 #pragma unroll
       for (int i = 0; i < NPART; ++i) v += pv[i];
-      a.y[n] = float_to_act_bits<DT>(v * (1.0f / Num::QS));
+      a.y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(v * (1.0f / Num::QS));
     }
   }
 }
 
-template <int DT, int GC>
+template <int DT, int GC, int MR>
 __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) {
-  extern __shared__ __attribute__((aligned(16))) float dec_smem[];
+  __shared__ __attribute__((aligned(16))) float dec_smem[one_lds(MR) / 4];
   const int t = blockIdx.x;
   int p = 0;
 #pragma unroll
@@ -654,12 +695,21 @@ __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) 
   constexpr int G128 = 2 << GC;
   constexpr int G64 = 1 << GC;
   constexpr int G32 = GC >= 1 ? (1 << (GC - 1)) : 1;  // the host uses T32 for groups >= 64 only
-  switch (a.cfg) {
-    case kCfgT128: dec_tile_one<DT, 128, G128, 8, 1>(a, tile, lds); break;
-    case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1>(a, tile, lds); break;
-    case kCfgT64Ring: dec_tile_one<DT, 64, G64, 4, 2>(a, tile, lds); break;
-    case kCfgT32: dec_tile_one<DT, 32, G32, 8, 1>(a, tile, lds); break;
-    default: dec_tile_one<DT, 32, G32, 4, 2>(a, tile, lds); break;
+  if constexpr (MR == 1) {
+    switch (a.cfg) {
+      case kCfgT128: dec_tile_one<DT, 128, G128, 8, 1, 1>(a, tile, lds); break;
+      case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1, 1>(a, tile, lds); break;
+      case kCfgT64Ring: dec_tile_one<DT, 64, G64, 4, 2, 1>(a, tile, lds); break;
+      case kCfgT32: dec_tile_one<DT, 32, G32, 8, 1, 1>(a, tile, lds); break;
+      default: dec_tile_one<DT, 32, G32, 4, 2, 1>(a, tile, lds); break;
+    }
+  } else {
+    // the host gives four-row launches single-round tilings only
+    switch (a.cfg) {
+      case kCfgT128: dec_tile_one<DT, 128, G128, 8, 1, MR>(a, tile, lds); break;
+      case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds); break;
+      default: dec_tile_one<DT, 32, G32, 8, 1, MR>(a, tile, lds); break;
+    }
   }
 }
 
@@ -720,7 +770,9 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int64_t tiles, bytes_per_wg;
   } items[W4_MAX_GROUPED];
   int gclass = -1;
-  bool cu_tiles = M == 1;  // every problem fits the one-workgroup-per-CU tilings
+  // every problem fits the one-workgroup-per-CU tilings (M <= 4; for M > 1
+  // only the single-round ones: K <= 8192, and K <= 4096 for group 32)
+  bool cu_tiles = M <= 4;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     if (!dec_fits_32bit(q.N, q.K) || q.group_size < 32 || !is_pow2(q.group_size)) return false;
@@ -731,6 +783,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     if (ldy != nullptr && ldy[i] < q.N) return false;
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
+    if (M > 1) cu_tiles = cu_tiles && q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096);
   }
   const int G = problems[0].group_size;
   // M == 1 tile width: about 128 KB of packed weights per workgroup (128
@@ -817,7 +870,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   if (cu_tiles) {
     dp.gs = std::min(ilog2(G) - 5, 4);  // dec_kernel_one: log2(group / 32), 4 = ">= 512"
     dp.threads = w4::kOneThreads;
-    dp.lds = w4::kOneLds;
+    dp.lds = 0;  // static in dec_kernel_one
   } else {
     dp.gs = (int)std::min(G / 32, 8);  // dec_kernel: steps per group, capped at 8
     dp.threads = w4::kDecThreads;
@@ -838,16 +891,24 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   return wgs > 0;
 }
 
-template <int DT>
-void dec_launch_one(const DecPlan& dp, hipStream_t st) {
+template <int DT, int MR>
+void dec_launch_one_mr(const DecPlan& dp, hipStream_t st) {
   const dim3 grid((unsigned)dp.wgs), block(w4::kOneThreads);
   switch (dp.gs) {
-    case 0: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 0>), grid, block, dp.lds, st, dp.g); break;
-    case 1: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 1>), grid, block, dp.lds, st, dp.g); break;
-    case 2: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 2>), grid, block, dp.lds, st, dp.g); break;
-    case 3: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 3>), grid, block, dp.lds, st, dp.g); break;
-    default: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 4>), grid, block, dp.lds, st, dp.g); break;
+    case 0: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 0, MR>), grid, block, dp.lds, st, dp.g); break;
+    case 1: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 1, MR>), grid, block, dp.lds, st, dp.g); break;
+    case 2: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 2, MR>), grid, block, dp.lds, st, dp.g); break;
+    case 3: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 3, MR>), grid, block, dp.lds, st, dp.g); break;
+    default: hipLaunchKernelGGL((w4::dec_kernel_one<DT, 4, MR>), grid, block, dp.lds, st, dp.g); break;
   }
+}
+
+template <int DT>
+void dec_launch_one(const DecPlan& dp, int64_t M, hipStream_t st) {
+  if (M == 1)
+    dec_launch_one_mr<DT, 1>(dp, st);
+  else
+    dec_launch_one_mr<DT, 4>(dp, st);
 }
 
 template <int DT, bool ONE, int MX>
@@ -864,7 +925,7 @@ void dec_launch_generic(const DecPlan& dp, hipStream_t st) {
 template <int DT>
 void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
   if (dp.cu_tiles)
-    dec_launch_one<DT>(dp, st);
+    dec_launch_one<DT>(dp, M, st);
   else if (M == 1)
     dec_launch_generic<DT, true, 1>(dp, st);
   else if (dp.mx == 4)

@@ -151,9 +151,9 @@ def test_grouped_matches_single(M):
         _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
     singles = [int4_hip.w4a16_matmul(x, *w) for x, w in zip(xs, ws)]
     for x, (qw, s, z), a, b in zip(xs, ws, outs, singles):
-        if M > 1:  # one problem per launch: same tiles, same bits
+        if M > 4:  # one problem per launch: same tiles, same bits
             assert torch.equal(a.view(torch.int16), b.view(torch.int16))
-        else:  # a lone M = 1 product narrows its tiles to reach more CUs
+        else:  # a lone M <= 4 product narrows its tiles to reach more CUs
             _check(b, x, qw, s, z, ref_unrounded=False, exact_w=True)
     again = int4_hip.w4a16_matmul_grouped(xs, ws)
     for a, b in zip(outs, again):
@@ -223,18 +223,21 @@ def test_decode_ragged_shapes(M, dtype, G):
         _check(int4_hip.w4a16_matmul(x, qw, s, z), x, qw, s, z, ref_unrounded=False, exact_w=True)
 
 
-# M == 1 one-workgroup-per-CU tilings: 128 columns (K <= 2048, short runs at
+# one-workgroup-per-CU tilings (M <= 4): 128 columns (K <= 2048, short runs at
 # K = 512), 64 columns (K = 4096, and rounds of 4 loads for group 32 at long
-# K), 32 columns (K = 6144 / 8192, rounds for K = 16384); partial last tiles;
-# group sizes from 32 to 1024 (the largest beyond the kernel's size classes)
+# K), 32 columns (K = 6144 / 8192, rounds for K = 16384, which M > 1 leaves to
+# the generic kernel); partial last tiles; group sizes from 32 to 1024 (the
+# largest beyond the kernel's size classes); M = 3 leaves one of the four
+# activation rows of the M > 1 kernel empty
+@pytest.mark.parametrize("M", [1, 3, 4])
 @pytest.mark.parametrize("G", [32, 64, 128, 1024])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_decode_cu_tiles(dtype, G):
+def test_decode_cu_tiles(dtype, G, M):
     shapes = [(N, K) for N, K in [(200, 2048), (8, 512), (96, 4096), (40, 8192), (48, 6144), (16, 16384)]
               if K % G == 0]
-    print(f"[decode-cu] G={G} {dtype} shapes={shapes}", flush=True)
+    print(f"[decode-cu] M={M} G={G} {dtype} shapes={shapes}", flush=True)
     ws = [_weights(N, K, G, seed=90 + i) for i, (N, K) in enumerate(shapes)]
-    xs = [randn((1, K), seed=100 + i, dtype=dtype).to(DEV) for i, (N, K) in enumerate(shapes)]
+    xs = [randn((M, K), seed=100 + i, dtype=dtype).to(DEV) for i, (N, K) in enumerate(shapes)]
     outs = int4_hip.w4a16_matmul_grouped(xs, ws)
     for x, (qw, s, z), y in zip(xs, ws, outs):
         _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
