@@ -229,10 +229,11 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   constexpr int D = DecChunk<VEC>::D;
   constexpr int NP = C / GS;  // correction points per chunk
   constexpr int R = ONE ? 1 : 4;
+  constexpr int RB = MX > 16 ? 2 : 1;    // 16-row MFMA blocks (MX = 32: rows 0..15, 16..31)
   constexpr int C4 = 4 * C;              // 16-byte activation slices per row and chunk
   constexpr int XL = ONE ? 1 : MX * C / 16;  // activation loads per chunk and lane
   static_assert(GS >= 1 && GS <= C && (C % GS) == 0, "correction interval");
-  static_assert(ONE || (XL >= 1 && MX <= C4 && MX <= 16), "activation staging");
+  static_assert(ONE || (XL >= 1 && (MX <= C4 || (MX == 32 && VEC == 4)) && MX <= 32), "activation staging");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -273,8 +274,15 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
       x_off[j] = m < M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)sl * 16u : kDecOOB;
     }
   }
-  const int mc = min(c, M - 1);
-  const int x_rd = mc * C4 + (kb ^ mc);  // read slot of step 0; step st adds 4 st inside the XOR
+  // read slot of step 0 for block b (row 16 b + c, rows past M repeat row
+  // M - 1); step st adds 4 st inside the XOR.  Slice s of row m sits at slot
+  // C4 m + (s ^ (m % C4)).
+  int x_rd[RB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) {
+    const int mc = min(16 * b + c, M - 1);
+    x_rd[b] = mc * C4 + (kb ^ (mc & (C4 - 1)));
+  }
   const uint32_t magic = dec_magic_vgpr<DT>();
   const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
 
@@ -320,13 +328,13 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  f32x4 acc[VEC];
-  f32x4 xs;
-  float tot[VEC][R];
+  f32x4 acc[RB][VEC];
+  f32x4 xs[RB];
+  float tot[VEC][RB * R];
 #pragma unroll
   for (int j = 0; j < VEC; ++j)
 #pragma unroll
-    for (int r = 0; r < R; ++r) tot[j][r] = 0.0f;
+    for (int r = 0; r < RB * R; ++r) tot[j][r] = 0.0f;
 
   auto compute_chunk = [&](const Chunk& ch) {
     if constexpr (ONE) {
@@ -340,7 +348,8 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
       for (int j = 0; j < XL; ++j) {
         const int f = 64 * j + lane;
         const int m = f / C4, sl = f % C4;
-        *reinterpret_cast<u32x4*>(xl + (wv * MX * C4 + m * C4 + (sl ^ m)) * 4) = dec_perm_x(ch.xv[j]);
+        *reinterpret_cast<u32x4*>(xl + (wv * MX * C4 + m * C4 + (sl ^ (m & (C4 - 1)))) * 4) =
+            dec_perm_x(ch.xv[j]);
       }
       __builtin_amdgcn_wave_barrier();
     }
@@ -349,18 +358,25 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
 #pragma unroll
       for (int i = 0; i < GS; ++i) {
         const int st = p * GS + i;
-        F xa;
-        if constexpr (ONE)
-          xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(xl + (wv * 64 + st * 4 + kb) * 4));
-        else
-          xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(
-                                         xl + (wv * MX * C4 + (x_rd ^ (4 * st))) * 4));
+        F xa[RB];
+        if constexpr (ONE) {
+          xa[0] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(xl + (wv * 64 + st * 4 + kb) * 4));
+        } else {
+#pragma unroll
+          for (int b = 0; b < RB; ++b)
+            xa[b] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(
+                                              xl + (wv * MX * C4 + (x_rd[b] ^ (4 * st))) * 4));
+        }
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
-          const F b = __builtin_bit_cast(F, Num::bvals(DecW<VEC>::get(ch.w[st], j), magic));
-          acc[j] = Mfma<DT>::m16(xa, b, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[j]);
+          const F bv = __builtin_bit_cast(F, Num::bvals(DecW<VEC>::get(ch.w[st], j), magic));
+#pragma unroll
+          for (int b = 0; b < RB; ++b)
+            acc[b][j] = Mfma<DT>::m16(xa[b], bv, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[b][j]);
         }
-        xs = Mfma<DT>::m16(xa, ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs);
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+          xs[b] = Mfma<DT>::m16(xa[b], ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs[b]);
       }
       // QS * sum x (q - z) = acc - (OFF + QS z) xs, one fma per accumulator
       // (OFF + QS z is exact for the integer zero points of the format);
@@ -372,12 +388,14 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
         sc[j] = ch.s[p].get(j);
       }
 #pragma unroll
-      for (int r = 0; r < R; ++r)
+      for (int b = 0; b < RB; ++b)
 #pragma unroll
-        for (int j = 0; j < VEC; ++j) {
-          const float u = __builtin_fmaf(-zc[j], xs[r], acc[j][r]);
-          tot[j][r] = __builtin_fmaf(sc[j], u, tot[j][r]);
-        }
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int j = 0; j < VEC; ++j) {
+            const float u = __builtin_fmaf(-zc[j], xs[b][r], acc[b][j][r]);
+            tot[j][b * R + r] = __builtin_fmaf(sc[j], u, tot[j][b * R + r]);
+          }
     }
     __builtin_amdgcn_wave_barrier();  // slots are rewritten by the next chunk
   };
@@ -404,8 +422,8 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   const int rstride = ONE ? M * TN : MX * C4 * 4;
   if (ONE ? kb == 0 : true) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int m = ONE ? 0 : kb * 4 + r;
+    for (int r = 0; r < RB * R; ++r) {
+      const int m = ONE ? 0 : (r / R) * 16 + kb * 4 + r % R;
       if (m < M) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) rbase[wv * rstride + m * TN + VEC * c + j] = tot[j][r];
@@ -727,7 +745,9 @@ __global__ __launch_bounds__(kDecThreads) void dec_kernel(DecGroupedArgs g) {
   // !ONE: [activation areas: 8 waves x MX x 4C x 16 B], reused for the reduction
   uint32_t* xl = reinterpret_cast<uint32_t*>(dec_smem);
   float* red = dec_smem + kDecWaves * 64 * 4;
-  if (a.vec == 4)
+  if constexpr (MX == 32)  // the host gives 32-row launches 64-column tiles only
+    dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4), MX>(a, tile, red, xl);
+  else if (a.vec == 4)
     dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4), MX>(a, tile, red, xl);
   else if (a.vec == 2)
     dec_tile<DT, 2, ONE, GS, MX>(a, tile, red, xl);
@@ -763,7 +783,7 @@ struct DecPlan {
 bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int64_t M,
               DecPlan& dp) {
   dp = DecPlan{};
-  if (count < 1 || count > W4_MAX_GROUPED || M < 1 || M > 16) return false;
+  if (count < 1 || count > W4_MAX_GROUPED || M < 1 || M > 32) return false;
   struct Item {
     int idx;
     int vec, cfg, tile_n;
@@ -827,6 +847,8 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
                       : (q.K <= 8192 ? w4::kCfgT32 : w4::kCfgT32Ring);
     } else if (q.N % 4 == 0 && qa % 16 == 0 && sa % 8 == 0 && za % 8 == 0 && q.K <= 4096) {
       vec = 4, tn = 64;
+    } else if (M > 16) {
+      return false;  // 32-row launches: 64-column tiles only
     } else if (q.N % 2 == 0 && qa % 8 == 0 && sa % 4 == 0 && za % 4 == 0) {
       vec = 2, tn = 32;
     }
@@ -880,7 +902,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     // 10.9 us with 8 rows against 12.2 / 12.4 us with 4, while launches of at
     // most one workgroup per CU are 6 % slower with 8); the rows fed to the
     // MFMA, and so every output bit, do not depend on it
-    dp.mx = (M <= 4 && wgs <= device_cu_count()) ? 4 : M <= 8 ? 8 : 16;
+    dp.mx = (M <= 4 && wgs <= device_cu_count()) ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : 32;
     bool narrow = false;  // a tile of vec < 4 has chunks of 8 steps (32 slices per row)
     for (int s = 0; s < count; ++s) narrow = narrow || dp.g.prob[s].vec < 4;
     // ONE: activation slots + reduction; M > 1: activation areas (at most
@@ -932,8 +954,10 @@ void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
     dec_launch_generic<DT, false, 4>(dp, st);
   else if (dp.mx == 8)
     dec_launch_generic<DT, false, 8>(dp, st);
-  else
+  else if (dp.mx == 16)
     dec_launch_generic<DT, false, 16>(dp, st);
+  else
+    dec_launch_generic<DT, false, 32>(dp, st);
 }
 
 }  // namespace

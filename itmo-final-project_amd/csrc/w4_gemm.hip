@@ -32,6 +32,13 @@ int w4_prefill_grouped_launch(const w4a16_problem* problems, int count, int x_dt
 static constexpr int64_t kSmallM = 64;
 // Decode-shaped products (activations staged in LDS) up to this M.
 static constexpr int64_t kDecodeM = 16;
+// Up to this M, products whose every operand fits the decode kernel's
+// 64-column tiles (K <= 4096, group >= 32, aligned, dense activation rows) take
+// it too (two 16-row MFMA blocks, no split-K partials); others the split-K path.
+static constexpr int64_t kDecode32M = 32;
+
+int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
+                     int x_dtype, int64_t M, hipStream_t st);
 
 // Every workspace starts with a W4_WORKSPACE_COUNTER_BYTES area of per-tile
 // arrival counters (zero before first use, left zero by every call), then
@@ -94,6 +101,11 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
   if (M <= kDecodeM)
     return w4_gemv_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
                           counters, scratch, scratch_bytes, st);
+  if (M <= kDecode32M && stride_xk == 1) {
+    const w4a16_problem q{x, qweight, scales, zeros, y, N, K, (int32_t)G, 0};
+    const int rc = w4_decode_launch(&q, &stride_xm, &ldy, 1, x_dtype, M, st);
+    if (rc != W4_ERR_UNSUPPORTED) return rc;
+  }
   if (M <= kSmallM) {
     const int rc = w4_prefill_fast_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros,
                                           (int)G, y, ldy, scratch, scratch_bytes, st);
@@ -145,9 +157,17 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
   const int rc = check_grouped(problems, count, M);
   if (rc != W4_OK) return rc;
   if (M > kDecodeM) {
-    // one launch when the products share their activation matrix, else one
-    // w4a16_gemm per problem, in order, on the stream (x rows of K elements)
+    // up to 32 rows, one decode launch when every problem fits its 64-column
+    // tiles; else one launch when the products share their activation matrix,
+    // else one w4a16_gemm per problem, in order, on the stream (x rows of K
+    // elements)
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (M <= kDecode32M) {
+      int64_t sxm[W4_MAX_GROUPED];
+      for (int i = 0; i < count; ++i) sxm[i] = problems[i].K;
+      const int drc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, M, st);
+      if (drc != W4_ERR_UNSUPPORTED) return drc;
+    }
     const int grc = w4_prefill_grouped_launch(problems, count, x_dtype, M, st);
     if (grc != W4_ERR_UNSUPPORTED || w4_last_error()[0] != '\0') return grc;
     for (int i = 0; i < count; ++i) {

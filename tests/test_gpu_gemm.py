@@ -33,9 +33,10 @@ DEV = "cuda"
 U_OUT = {torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
 
 
-def _decode(M: int, G: int) -> bool:
-    """True when w4a16_matmul takes the factored decode kernel (dense rows)."""
-    return M <= 16 and G >= 32
+def _decode(M: int, G: int, N: int = 0, K: int = 1 << 30) -> bool:
+    """True when w4a16_matmul takes the factored decode kernel (dense, aligned
+    rows): M <= 16, or M <= 32 with 64-column tiles (N % 4 == 0, K <= 4096)."""
+    return G >= 32 and (M <= 16 or (M <= 32 and N % 4 == 0 and K <= 4096))
 
 
 def _check(out: torch.Tensor, x: torch.Tensor, qw, s, z, ref_unrounded: bool = True, exact_w: bool = False):
@@ -87,7 +88,7 @@ def test_w4a16_matmul(M, NK, dtype):
 
 # split-K regime over the block's shapes and the three group sizes
 @pytest.mark.parametrize("G", [128, 64, 32])
-@pytest.mark.parametrize("M", [2, 4, 8, 16, 32, 64])
+@pytest.mark.parametrize("M", [2, 4, 8, 16, 24, 32, 64])
 @pytest.mark.parametrize("NK", [(2048, 2048), (512, 2048), (2048, 8192)])
 def test_split_k_regime(M, NK, G):
     N, K = NK
@@ -95,7 +96,7 @@ def test_split_k_regime(M, NK, G):
     qw, s, z = _weights(N, K, G, seed=7 * N + K + G)
     x = randn((M, K), seed=100 + M).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
-    _check(out, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, G))
+    _check(out, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, G, N, K))
     # bit-identical repeat runs, with the workspace poisoned in between
     junk = torch.full((64 << 20,), float("nan"), device=DEV)
     del junk
