@@ -237,7 +237,7 @@ def hbm_read_ceiling(dev, stream, block_bytes_: int, nsets: int) -> dict | None:
 
 
 PROFILE = ROOT / "profiles" / "dec_kernel_one_decode_block_m1.md"
-ROOFLINE_KERNEL = "dec_kernel_one<0, 2>"
+ROOFLINE_KERNEL = "dec_kernel_one<0, 2, 1>"
 
 
 def summarize_prof(d: Path, kernel: str = ROOFLINE_KERNEL) -> str:

@@ -100,7 +100,7 @@ size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
  * ldy (>= N), unit column stride.  Launch regimes (same boundaries as the
  * reference): M <= 16 (group sizes >= 32) the factored decode kernel in one
  * launch, no workspace, and up to M = 32 when every operand fits its 64-column
- * tiles (K <= 4096, N % 4 == 0, 16-byte aligned dense rows); otherwise
+ * tiles (K <= 4096, N % 4 == 0, group >= 64, 16-byte aligned dense rows); otherwise
  * M <= 64 (and group sizes < 32) split-K with fp32 partials in `workspace`
  * and a fixed-order reduce kernel; M > 64 tiled
  * MFMA GEMM, itself split over K with the same partials-and-reduce scheme
@@ -147,7 +147,7 @@ size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, i
  *   fp32 partials are summed, in split order, by the last workgroup of each
  *   column tile to finish (in `workspace`).
  *   17 <= M <= 32: the same single decode launch when every problem fits its
- *   64-column tiles (K <= 4096, N % 4 == 0, 16-byte aligned).
+ *   64-column tiles (K <= 4096, N % 4 == 0, group >= 64, 16-byte aligned).
  *   Otherwise, M > 16: problems that share one activation matrix (same x pointer, K and
  *   group size; at most 4) run as ONE launch of the prefill kernel (no
  *   split-K, the tiles of all problems side by side) when the library's

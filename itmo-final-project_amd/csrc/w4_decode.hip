@@ -839,6 +839,9 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     const w4a16_problem& q = problems[i];
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     int vec = 1, cfg = 0, tn = 16;
+    // with group 32 the per-step correction of 32 rows costs more than the
+    // split-K path saves (7-launch block at M = 32: 82.0 against 76.5 us)
+    if (M > 16 && q.group_size < 64) return false;
     if (cu_tiles) {
       vec = 4;
       tn = one_width(q.K, level);

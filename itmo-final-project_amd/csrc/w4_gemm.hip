@@ -33,7 +33,7 @@ static constexpr int64_t kSmallM = 64;
 // Decode-shaped products (activations staged in LDS) up to this M.
 static constexpr int64_t kDecodeM = 16;
 // Up to this M, products whose every operand fits the decode kernel's
-// 64-column tiles (K <= 4096, group >= 32, aligned, dense activation rows) take
+// 64-column tiles (K <= 4096, group >= 64, aligned, dense activation rows) take
 // it too (two 16-row MFMA blocks, no split-K partials); others the split-K path.
 static constexpr int64_t kDecode32M = 32;
 

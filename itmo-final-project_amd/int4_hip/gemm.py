@@ -6,7 +6,7 @@ reference (int4_triton/gemm.py:223-317):
   * M <= 16:       decode kernel, one launch, no workspace (group sizes >= 32
                    and dense rows; else split-K with a fixed-order reduce);
                    up to M = 32 for operands that fit its 64-column tiles
-                   (K <= 4096, N % 4 == 0);
+                   (K <= 4096, N % 4 == 0, group >= 64);
   * 17 <= M <= 64: otherwise split-K with fp32 partials and a fixed-order
                    reduce kernel;
   * M > 64:        tiled MFMA GEMM writing the output dtype directly, split
@@ -131,7 +131,7 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
 
     ``weights[i]`` is a ``(qweight, scales, zeros)`` triple.  All ``xs[i]`` share
     dtype and the leading size M.  For M <= 16 every problem runs in one decode
-    launch, up to M = 32 too when every problem has K <= 4096 and N % 4 == 0;
+    launch, up to M = 32 too when every problem has K <= 4096, N % 4 == 0 and G >= 64;
     for larger M, products of one shared activation tensor (q/k/v,
     gate/up: pass the same tensor) run as one prefill launch when the library's
     plan allows it, else one launch each.  This fuses the per-linear launches

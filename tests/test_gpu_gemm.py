@@ -35,8 +35,9 @@ U_OUT = {torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
 
 def _decode(M: int, G: int, N: int = 0, K: int = 1 << 30) -> bool:
     """True when w4a16_matmul takes the factored decode kernel (dense, aligned
-    rows): M <= 16, or M <= 32 with 64-column tiles (N % 4 == 0, K <= 4096)."""
-    return G >= 32 and (M <= 16 or (M <= 32 and N % 4 == 0 and K <= 4096))
+    rows): M <= 16, or M <= 32 with 64-column tiles (N % 4 == 0, K <= 4096,
+    group >= 64)."""
+    return G >= 32 and (M <= 16 or (M <= 32 and G >= 64 and N % 4 == 0 and K <= 4096))
 
 
 def _check(out: torch.Tensor, x: torch.Tensor, qw, s, z, ref_unrounded: bool = True, exact_w: bool = False):
