@@ -480,11 +480,16 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
 // the rows 0..3 of their columns, each corrected with its own activation sum.
 constexpr int kOneWaves = 16;
 constexpr int kOneThreads = 64 * kOneWaves;
-// per wave: activations MR KB, scales 1 KB, zeros 1 KB; then the reduction
-// area, MR x 128 floats per wave
-constexpr int one_wave_lds(int mr) { return mr * 1024 + 2048; }
+// per wave: activations (1 KB per row; 512 B per row for MR = 8, which has
+// the 128- and 64-column tilings only), scales 1 KB, zeros 1 KB; then the
+// reduction area, MR x 128 floats per wave (MR = 8: each wave's partials go
+// to its own activation area, 8 x 512 B, which only it has used)
+constexpr int one_xrow(int mr) { return mr == 8 ? 512 : 1024; }
+constexpr int one_wave_lds(int mr) { return mr * one_xrow(mr) + 2048; }
 constexpr int one_red_offset(int mr) { return kOneWaves * one_wave_lds(mr); }
-constexpr int one_lds(int mr) { return one_red_offset(mr) + kOneWaves * mr * 128 * (int)sizeof(float); }
+constexpr int one_lds(int mr) {
+  return one_red_offset(mr) + (mr == 8 ? 0 : kOneWaves * mr * 128 * (int)sizeof(float));
+}
 
 template <int DT, int TW, int GSI, int NL, int D, int MR>
 __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t* lds) {
@@ -500,8 +505,10 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   constexpr int XE = NL * RPS;                           // activation entries (8 k) per round and row
   constexpr int XLD = (MR * XE + 63) / 64;               // activation loads per round and lane
   constexpr int WLDS = one_wave_lds(MR);
-  static_assert(MR == 1 || MR == 4, "activation rows");
-  static_assert(MR == 1 || D == 1, "four rows: single-round tilings only");
+  static_assert(MR == 1 || MR == 4 || MR == 8, "activation rows");
+  static_assert(MR == 1 || D == 1, "several rows: single-round tilings only");
+  static_assert(MR != 8 || (TW != 32 && NL * SLOTS * 16 <= one_xrow(8)), "eight rows: 128 / 64 columns");
+  constexpr int RE = MR < 4 ? MR : 4;  // result rows per lane (accumulator elements used)
   static_assert(XE <= 64 && NP * LPG <= 64 && NL * SLOTS * 16 <= 1024, "per-wave staging area");
   static_assert(GSI >= 1 && (NL % GS) == 0, "correction interval");
 
@@ -513,15 +520,17 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   // activation row of this lane's A-operand row
   int a_slot = lr;
   if constexpr (TW == 128) a_slot = (((lane & 15) >> 3) == ((lane >> 4) & 1)) ? (lane >> 5) : 2;
-  const int a_row = MR == 1 ? 0 : (lane & 3);
+  const int a_row = lane & (MR - 1);
+  // activation row of accumulator element e of this lane (A rows 4 (lane / 16) + e)
+  const int r_base = MR == 8 ? 4 * ((lane >> 4) & 1) : 0;
   // result owners: output quad oq (columns 4 oq .. 4 oq + 3) and part
   bool owner;
   int oq, part = 0;
   if constexpr (TW == 128) {
-    owner = lane < 16 || (lane >= 32 && lane < 48);
+    owner = MR == 8 || lane < 16 || (lane >= 32 && lane < 48);
     oq = lane < 32 ? (lane & 15) : 16 + (lane & 15);
   } else if constexpr (TW == 64) {
-    owner = lane < 16;
+    owner = MR == 8 ? lane < 32 : lane < 16;
     oq = lane & 15;
   } else {
     owner = lane < 8 || (lane >= 40 && lane < 48);
@@ -557,14 +566,15 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   const uint32_t sz_oob = lane < NP * LPG ? 0u : kDecOOB;
   const uint32_t sz_lane = (uint32_t)(lane / LPG) * (uint32_t)N * 2u + (uint32_t)(n0 * 2 + (lane % LPG) * 16);
   uint8_t* x_lds = lds + wv * WLDS;
-  uint8_t* s_lds = x_lds + MR * 1024;
+  uint8_t* s_lds = x_lds + MR * one_xrow(MR);
   uint8_t* z_lds = s_lds + 1024;
   const uint32_t magic = dec_magic_vgpr<DT>();
   const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
   if constexpr (TW == 128) {
     // the zero A slots (2 and 3 of every step and row) are never rewritten
-    if (lane < 2 * NL * MR) {
-      const int m = lane / (2 * NL), e = lane % (2 * NL);
+#pragma unroll
+    for (int f = lane; f < 2 * NL * MR; f += 64) {
+      const int m = f / (2 * NL), e = f % (2 * NL);
       *reinterpret_cast<u32x4*>(x_lds + ((m * NL + (e >> 1)) * SLOTS + 2 + (e & 1)) * 16) = u32x4{0u, 0u, 0u, 0u};
     }
   }
@@ -594,11 +604,11 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
 
   f32x4 acc[4];
   f32x4 xs;
-  float tot[4][MR];
+  float tot[4][RE];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int m = 0; m < MR; ++m) tot[j][m] = 0.f;
+    for (int e = 0; e < RE; ++e) tot[j][e] = 0.f;
 
   auto compute_round = [&](const Round& r, int sb) {
     // stage the round's activations (permuted), scales and zeros
@@ -634,9 +644,9 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
         const float sj = half_bits_to_float((uint16_t)(sv[j >> 1] >> (16 * (j & 1))));
         const float zj = half_bits_to_float((uint16_t)(zv[j >> 1] >> (16 * (j & 1))));
 #pragma unroll
-        for (int m = 0; m < MR; ++m) {
-          const float u = __builtin_fmaf(-zj, Num::QS * xs[m], acc[j][m] - Num::OFF * xs[m]);
-          tot[j][m] = __builtin_fmaf(sj, u, tot[j][m]);
+        for (int e = 0; e < RE; ++e) {
+          const float u = __builtin_fmaf(-zj, Num::QS * xs[e], acc[j][e] - Num::OFF * xs[e]);
+          tot[j][e] = __builtin_fmaf(sj, u, tot[j][e]);
         }
       }
     }
@@ -662,13 +672,15 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     }
   }
 
-  // cross-wave (T32: and even/odd row) reduction in a fixed order
-  float* red = reinterpret_cast<float*>(lds + one_red_offset(MR));
+  // cross-wave (T32: and even/odd row) reduction in a fixed order; partials
+  // of wave w, row m at red + w * RSTR + m * 128
+  constexpr int RSTR = MR == 8 ? WLDS / 4 : MR * 128;  // floats
+  float* red = reinterpret_cast<float*>(lds + (MR == 8 ? 0 : one_red_offset(MR)));
   if (owner) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m)
+    for (int e = 0; e < RE; ++e)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) red[(wv * MR + m) * 128 + part * 32 + 4 * oq + j] = tot[j][m];
+      for (int j = 0; j < 4; ++j) red[wv * RSTR + (r_base + e) * 128 + part * 32 + 4 * oq + j] = tot[j][e];
   }
   __syncthreads();
   if (tid < MR * TW) {
@@ -681,7 +693,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       float pv[NPART];
 #pragma unroll
       for (int w = 0; w < kOneWaves; ++w) {
-        const float* rw = red + (w * MR + m) * 128;
+        const float* rw = red + w * RSTR + m * 128;
         if constexpr (TW == 32) {
           pv[2 * w] = rw[nl];
           pv[2 * w + 1] = rw[32 + nl];
@@ -721,13 +733,19 @@ __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) 
       case kCfgT32: dec_tile_one<DT, 32, G32, 8, 1, 1>(a, tile, lds); break;
       default: dec_tile_one<DT, 32, G32, 4, 2, 1>(a, tile, lds); break;
     }
-  } else {
+  } else if constexpr (MR == 4) {
     // the host gives four-row launches single-round tilings only
     switch (a.cfg) {
       case kCfgT128: dec_tile_one<DT, 128, G128, 8, 1, MR>(a, tile, lds); break;
       case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds); break;
       default: dec_tile_one<DT, 32, G32, 8, 1, MR>(a, tile, lds); break;
     }
+  } else {
+    // eight rows: the 128- and 64-column tilings only
+    if (a.cfg == kCfgT128)
+      dec_tile_one<DT, 128, G128, 8, 1, MR>(a, tile, lds);
+    else
+      dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds);
   }
 }
 
@@ -790,9 +808,10 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int64_t tiles, bytes_per_wg;
   } items[W4_MAX_GROUPED];
   int gclass = -1;
-  // every problem fits the one-workgroup-per-CU tilings (M <= 4; for M > 1
-  // only the single-round ones: K <= 8192, and K <= 4096 for group 32)
-  bool cu_tiles = M <= 4;
+  // every problem fits the one-workgroup-per-CU tilings (M <= 8; for M > 1
+  // only the single-round ones: K <= 8192, and K <= 4096 for group 32; for
+  // M > 4 only the 128- and 64-column ones: K <= 4096)
+  bool cu_tiles = M <= 8;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     if (!dec_fits_32bit(q.N, q.K) || q.group_size < 32 || !is_pow2(q.group_size)) return false;
@@ -804,6 +823,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
     if (M > 1) cu_tiles = cu_tiles && q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096);
+    if (M > 4) cu_tiles = cu_tiles && q.K <= 4096;
   }
   const int G = problems[0].group_size;
   // M == 1 tile width: about 128 KB of packed weights per workgroup (128
@@ -817,7 +837,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     for (int l = 0; l < level; ++l) {
       if (tn == 128)
         tn = 64;
-      else if (tn == 64 && G >= 64 && K <= 8192)
+      else if (tn == 64 && G >= 64 && K <= 8192 && M <= 4)  // eight rows: no 32-column tiling
         tn = 32;
     }
     return tn;
@@ -932,8 +952,10 @@ template <int DT>
 void dec_launch_one(const DecPlan& dp, int64_t M, hipStream_t st) {
   if (M == 1)
     dec_launch_one_mr<DT, 1>(dp, st);
-  else
+  else if (M <= 4)
     dec_launch_one_mr<DT, 4>(dp, st);
+  else
+    dec_launch_one_mr<DT, 8>(dp, st);
 }
 
 template <int DT, bool ONE, int MX>
