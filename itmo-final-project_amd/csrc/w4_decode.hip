@@ -480,15 +480,16 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
 // the rows 0..3 of their columns, each corrected with its own activation sum.
 constexpr int kOneWaves = 16;
 constexpr int kOneThreads = 64 * kOneWaves;
-// per wave: activations (1 KB per row; 512 B per row for MR = 8, which has
-// the 128- and 64-column tilings only), scales 1 KB, zeros 1 KB; then the
-// reduction area, MR x 128 floats per wave (MR = 8: each wave's partials go
-// to its own activation area, 8 x 512 B, which only it has used)
-constexpr int one_xrow(int mr) { return mr == 8 ? 512 : 1024; }
+// per wave: activations (1 KB per row; 512 B per row for MR = 8 / 16, which
+// have the 128- and 64-column / the 64-column tilings only), scales 1 KB,
+// zeros 1 KB; then the reduction area, MR x 128 floats per wave (MR = 8 /
+// 16: each wave's partials go to its own activation area, which only it has
+// used: 8 x 128 floats in 8 x 512 B, 16 x 64 floats in 16 x 512 B)
+constexpr int one_xrow(int mr) { return mr >= 8 ? 512 : 1024; }
 constexpr int one_wave_lds(int mr) { return mr * one_xrow(mr) + 2048; }
 constexpr int one_red_offset(int mr) { return kOneWaves * one_wave_lds(mr); }
 constexpr int one_lds(int mr) {
-  return one_red_offset(mr) + (mr == 8 ? 0 : kOneWaves * mr * 128 * (int)sizeof(float));
+  return one_red_offset(mr) + (mr >= 8 ? 0 : kOneWaves * mr * 128 * (int)sizeof(float));
 }
 
 template <int DT, int TW, int GSI, int NL, int D, int MR>
@@ -505,7 +506,8 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   constexpr int XE = NL * RPS;                           // activation entries (8 k) per round and row
   constexpr int XLD = (MR * XE + 63) / 64;               // activation loads per round and lane
   constexpr int WLDS = one_wave_lds(MR);
-  static_assert(MR == 1 || MR == 4 || MR == 8, "activation rows");
+  static_assert(MR == 1 || MR == 4 || MR == 8 || MR == 16, "activation rows");
+  static_assert(MR != 16 || TW == 64, "sixteen rows: 64 columns (all A rows distinct)");
   static_assert(MR == 1 || D == 1, "several rows: single-round tilings only");
   static_assert(MR != 8 || (TW != 32 && NL * SLOTS * 16 <= one_xrow(8)), "eight rows: 128 / 64 columns");
   constexpr int RE = MR < 4 ? MR : 4;  // result rows per lane (accumulator elements used)
@@ -522,7 +524,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   if constexpr (TW == 128) a_slot = (((lane & 15) >> 3) == ((lane >> 4) & 1)) ? (lane >> 5) : 2;
   const int a_row = lane & (MR - 1);
   // activation row of accumulator element e of this lane (A rows 4 (lane / 16) + e)
-  const int r_base = MR == 8 ? 4 * ((lane >> 4) & 1) : 0;
+  const int r_base = MR == 16 ? 4 * (lane >> 4) : MR == 8 ? 4 * ((lane >> 4) & 1) : 0;
   // result owners: output quad oq (columns 4 oq .. 4 oq + 3) and part
   bool owner;
   int oq, part = 0;
@@ -530,7 +532,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     owner = MR == 8 || lane < 16 || (lane >= 32 && lane < 48);
     oq = lane < 32 ? (lane & 15) : 16 + (lane & 15);
   } else if constexpr (TW == 64) {
-    owner = MR == 8 ? lane < 32 : lane < 16;
+    owner = MR == 16 ? true : MR == 8 ? lane < 32 : lane < 16;
     oq = lane & 15;
   } else {
     owner = lane < 8 || (lane >= 40 && lane < 48);
@@ -674,13 +676,15 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
 
   // cross-wave (T32: and even/odd row) reduction in a fixed order; partials
   // of wave w, row m at red + w * RSTR + m * 128
-  constexpr int RSTR = MR == 8 ? WLDS / 4 : MR * 128;  // floats
-  float* red = reinterpret_cast<float*>(lds + (MR == 8 ? 0 : one_red_offset(MR)));
+  // (MR = 16: rows 64 floats apart, the tile is 64 columns)
+  constexpr int RSTR = MR >= 8 ? WLDS / 4 : MR * 128;  // floats
+  constexpr int RROW = MR == 16 ? 64 : 128;
+  float* red = reinterpret_cast<float*>(lds + (MR >= 8 ? 0 : one_red_offset(MR)));
   if (owner) {
 #pragma unroll
     for (int e = 0; e < RE; ++e)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) red[wv * RSTR + (r_base + e) * 128 + part * 32 + 4 * oq + j] = tot[j][e];
+      for (int j = 0; j < 4; ++j) red[wv * RSTR + (r_base + e) * RROW + part * 32 + 4 * oq + j] = tot[j][e];
   }
   __syncthreads();
   if (tid < MR * TW) {
@@ -693,7 +697,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       float pv[NPART];
 #pragma unroll
       for (int w = 0; w < kOneWaves; ++w) {
-        const float* rw = red + w * RSTR + m * 128;
+        const float* rw = red + w * RSTR + m * RROW;
         if constexpr (TW == 32) {
           pv[2 * w] = rw[nl];
           pv[2 * w + 1] = rw[32 + nl];
@@ -740,12 +744,15 @@ __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) 
       case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds); break;
       default: dec_tile_one<DT, 32, G32, 8, 1, MR>(a, tile, lds); break;
     }
-  } else {
+  } else if constexpr (MR == 8) {
     // eight rows: the 128- and 64-column tilings only
     if (a.cfg == kCfgT128)
       dec_tile_one<DT, 128, G128, 8, 1, MR>(a, tile, lds);
     else
       dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds);
+  } else {
+    // sixteen rows: the 64-column tiling only
+    dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds);
   }
 }
 
@@ -808,10 +815,11 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int64_t tiles, bytes_per_wg;
   } items[W4_MAX_GROUPED];
   int gclass = -1;
-  // every problem fits the one-workgroup-per-CU tilings (M <= 8; for M > 1
+  // every problem fits the one-workgroup-per-CU tilings (M <= 16; for M > 1
   // only the single-round ones: K <= 8192, and K <= 4096 for group 32; for
-  // M > 4 only the 128- and 64-column ones: K <= 4096)
-  bool cu_tiles = M <= 8;
+  // M > 4 only the 128- and 64-column ones: K <= 4096; for M > 8 the
+  // 64-column one)
+  bool cu_tiles = M <= 16;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     if (!dec_fits_32bit(q.N, q.K) || q.group_size < 32 || !is_pow2(q.group_size)) return false;
@@ -833,7 +841,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   // grid still fits one workgroup per CU, so a lone small linear spreads over
   // the chip instead of a few CUs; a decoder block's 7 linears stay at level 0.
   auto one_width = [&](int64_t K, int level) {
-    int tn = K <= 2048 ? 128 : (K <= 4096 || G < 64) ? 64 : 32;
+    int tn = (K <= 2048 && M <= 8) ? 128 : (K <= 4096 || G < 64) ? 64 : 32;  // 16 rows: 64 only
     for (int l = 0; l < level; ++l) {
       if (tn == 128)
         tn = 64;
@@ -954,8 +962,10 @@ void dec_launch_one(const DecPlan& dp, int64_t M, hipStream_t st) {
     dec_launch_one_mr<DT, 1>(dp, st);
   else if (M <= 4)
     dec_launch_one_mr<DT, 4>(dp, st);
-  else
+  else if (M <= 8)
     dec_launch_one_mr<DT, 8>(dp, st);
+  else
+    dec_launch_one_mr<DT, 16>(dp, st);
 }
 
 template <int DT, bool ONE, int MX>

@@ -153,9 +153,9 @@ def test_grouped_matches_single(M):
         _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
     singles = [int4_hip.w4a16_matmul(x, *w) for x, w in zip(xs, ws)]
     for x, (qw, s, z), a, b in zip(xs, ws, outs, singles):
-        if M > 8:  # one problem per launch: same tiles, same bits
+        if M > 16:  # one problem per launch: same tiles, same bits
             assert torch.equal(a.view(torch.int16), b.view(torch.int16))
-        else:  # a lone M <= 8 product may take other tiles (another summation order)
+        else:  # a lone product may take other tiles (another summation order)
             _check(b, x, qw, s, z, ref_unrounded=False, exact_w=True)
     again = int4_hip.w4a16_matmul_grouped(xs, ws)
     for a, b in zip(outs, again):
@@ -229,9 +229,10 @@ def test_decode_ragged_shapes(M, dtype, G):
 # K = 512), 64 columns (K = 4096, and rounds of 4 loads for group 32 at long
 # K), 32 columns (K = 6144 / 8192, rounds for K = 16384, which M > 1 leaves to
 # the generic kernel); partial last tiles; group sizes from 32 to 1024 (the
-# largest beyond the kernel's size classes); M = 3 / 6 leave activation rows
-# of the four- and eight-row kernels empty (M > 4: K <= 4096 tilings only)
-@pytest.mark.parametrize("M", [1, 3, 4, 6, 8])
+# largest beyond the kernel's size classes); M = 3 / 6 / 11 leave activation
+# rows of the four-, eight- and sixteen-row kernels empty (M > 4: K <= 4096
+# tilings only, M > 8: 64 columns)
+@pytest.mark.parametrize("M", [1, 3, 4, 6, 8, 11, 16])
 @pytest.mark.parametrize("G", [32, 64, 128, 1024])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_decode_cu_tiles(dtype, G, M):
