@@ -480,12 +480,12 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
 // the rows 0..3 of their columns, each corrected with its own activation sum.
 constexpr int kOneWaves = 16;
 constexpr int kOneThreads = 64 * kOneWaves;
-// per wave: activations (1 KB per row; 512 B per row for MR = 8 / 16, which
-// have the 128- and 64-column / the 64-column tilings only), scales 1 KB,
-// zeros 1 KB; then the reduction area, MR x 128 floats per wave (MR = 8 /
-// 16: each wave's partials go to its own activation area, which only it has
-// used: 8 x 128 floats in 8 x 512 B, 16 x 64 floats in 16 x 512 B)
-constexpr int one_xrow(int mr) { return mr >= 8 ? 512 : 1024; }
+// per wave: activations (1 KB per row; 512 B per row for MR = 16, which has
+// the 64-column tiling only), scales 1 KB, zeros 1 KB; then the reduction
+// area, MR x 128 floats per wave (MR = 8 / 16: each wave's partials go to
+// its own activation area, which only it has used: 8 x 128 floats in 8 KB,
+// 16 x 64 floats in 16 x 512 B)
+constexpr int one_xrow(int mr) { return mr == 16 ? 512 : 1024; }
 constexpr int one_wave_lds(int mr) { return mr * one_xrow(mr) + 2048; }
 constexpr int one_red_offset(int mr) { return kOneWaves * one_wave_lds(mr); }
 constexpr int one_lds(int mr) {
@@ -509,7 +509,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   static_assert(MR == 1 || MR == 4 || MR == 8 || MR == 16, "activation rows");
   static_assert(MR != 16 || TW == 64, "sixteen rows: 64 columns (all A rows distinct)");
   static_assert(MR == 1 || D == 1, "several rows: single-round tilings only");
-  static_assert(MR != 8 || (TW != 32 && NL * SLOTS * 16 <= one_xrow(8)), "eight rows: 128 / 64 columns");
+  static_assert(NL * SLOTS * 16 <= one_xrow(MR), "per-row staging");
   constexpr int RE = MR < 4 ? MR : 4;  // result rows per lane (accumulator elements used)
   static_assert(XE <= 64 && NP * LPG <= 64 && NL * SLOTS * 16 <= 1024, "per-wave staging area");
   static_assert(GSI >= 1 && (NL % GS) == 0, "correction interval");
@@ -534,6 +534,12 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   } else if constexpr (TW == 64) {
     owner = MR == 16 ? true : MR == 8 ? lane < 32 : lane < 16;
     oq = lane & 15;
+  } else if constexpr (MR == 8) {
+    // lane groups 0 / 1: even rows (columns 0..7 of the result), rows 0..3 /
+    // 4..7; groups 2 / 3: odd rows (columns 8..15)
+    owner = ((lane & 15) < 8) == (lane < 32);
+    oq = lane & 7;
+    part = lane >= 32 ? 1 : 0;
   } else {
     owner = lane < 8 || (lane >= 40 && lane < 48);
     oq = lane & 7;
@@ -745,11 +751,12 @@ __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) 
       default: dec_tile_one<DT, 32, G32, 8, 1, MR>(a, tile, lds); break;
     }
   } else if constexpr (MR == 8) {
-    // eight rows: the 128- and 64-column tilings only
-    if (a.cfg == kCfgT128)
-      dec_tile_one<DT, 128, G128, 8, 1, MR>(a, tile, lds);
-    else
-      dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds);
+    // single-round tilings only, as for four rows
+    switch (a.cfg) {
+      case kCfgT128: dec_tile_one<DT, 128, G128, 8, 1, MR>(a, tile, lds); break;
+      case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds); break;
+      default: dec_tile_one<DT, 32, G32, 8, 1, MR>(a, tile, lds); break;
+    }
   } else {
     // sixteen rows: the 64-column tiling only
     dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds);
@@ -817,8 +824,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   int gclass = -1;
   // every problem fits the one-workgroup-per-CU tilings (M <= 16; for M > 1
   // only the single-round ones: K <= 8192, and K <= 4096 for group 32; for
-  // M > 4 only the 128- and 64-column ones: K <= 4096; for M > 8 the
-  // 64-column one)
+  // M > 8 only the 64-column one: K <= 4096)
   bool cu_tiles = M <= 16;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
@@ -831,7 +837,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
     if (M > 1) cu_tiles = cu_tiles && q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096);
-    if (M > 4) cu_tiles = cu_tiles && q.K <= 4096;
+    if (M > 8) cu_tiles = cu_tiles && q.K <= 4096;
   }
   const int G = problems[0].group_size;
   // M == 1 tile width: about 128 KB of packed weights per workgroup (128
@@ -845,7 +851,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     for (int l = 0; l < level; ++l) {
       if (tn == 128)
         tn = 64;
-      else if (tn == 64 && G >= 64 && K <= 8192 && M <= 4)  // eight rows: no 32-column tiling
+      else if (tn == 64 && G >= 64 && K <= 8192 && M <= 8)  // sixteen rows: no 32-column tiling
         tn = 32;
     }
     return tn;
