@@ -75,7 +75,7 @@ def _weights(N, K, G, seed, wdtype=torch.bfloat16):
 
 # int4_triton tests/test_kernels.py:47-60 (M x shape x dtype grid)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("M", [1, 7, 128, 512, 2048])
+@pytest.mark.parametrize("M", [1, 7, 24, 128, 512, 2048])
 @pytest.mark.parametrize("NK", [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192), (300, 256)])
 def test_w4a16_matmul(M, NK, dtype):
     N, K = NK
@@ -84,7 +84,7 @@ def test_w4a16_matmul(M, NK, dtype):
     x = randn((M, K), seed=M, dtype=dtype).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
     assert out.dtype == dtype and out.shape == (M, N)
-    _check(out, x, qw, s, z, exact_w=_decode(M, 128))
+    _check(out, x, qw, s, z, exact_w=_decode(M, 128, N, K))
 
 
 # split-K regime over the block's shapes and the three group sizes
@@ -298,18 +298,20 @@ def test_prefill_split_k_bit_identical(M, NK):
 @pytest.mark.parametrize("G", [32, 128])
 @pytest.mark.parametrize("M,K,Ns", [(130, 512, (256, 64, 64)), (300, 256, (1024, 256, 256)),
                                      (512, 512, (192, 72, 120)), (40, 512, (128, 64)),
-                                     (128, 2048, (2048, 512, 512))])
+                                     (128, 2048, (2048, 512, 512)), (24, 2048, (2048, 512, 512))])
 def test_grouped_shared_activation(M, K, Ns, G):
     print(f"[grouped-prefill] M={M} K={K} Ns={Ns} G={G}", flush=True)
     ws = [_weights(N, K, G, seed=400 + i) for i, N in enumerate(Ns)]
     x = randn((M, K), seed=410 + M).to(DEV)
+    # M <= 32 with K <= 4096 and G >= 64: one decode launch (exact W_hat)
+    ew = all(_decode(M, G, N, K) for N in Ns)
     outs = int4_hip.w4a16_matmul_grouped([x] * len(Ns), ws)
     for (qw, s, z), y in zip(ws, outs):
-        _check(y, x, qw, s, z)
+        _check(y, x, qw, s, z, ref_unrounded=not ew, exact_w=ew)
     again = int4_hip.w4a16_matmul_grouped([x] * len(Ns), ws)
     for a, b in zip(outs, again):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     xs = [randn((M, K), seed=420 + i).to(DEV) for i in range(len(Ns))]
     mixed = int4_hip.w4a16_matmul_grouped(xs, ws)
     for xi, (qw, s, z), y in zip(xs, ws, mixed):
-        _check(y, xi, qw, s, z)
+        _check(y, xi, qw, s, z, ref_unrounded=not ew, exact_w=ew)
