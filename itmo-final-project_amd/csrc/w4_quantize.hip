@@ -255,7 +255,9 @@ __global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
           // 32-bit offsets: the host routes only weights below 2^31 bytes here
           const uint32_t off = n < N ? ((uint32_t)n * (uint32_t)swn + (uint32_t)(g * G + seg * 8)) * 2u
                                      : 0x80000000u;
-          raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0);
+          // non-temporal (cache policy bit 1): every weight byte is read
+          // once (block 64.4 -> 61.8 us against the default policy)
+          raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 2);
         } else {
           uint16_t e[8];
 #pragma unroll
