@@ -268,11 +268,12 @@ def test_prefill_group_sizes_and_partial_tiles(M, G, NK):
 
 # shapes whose static plan runs 32-row tiles as workgroups of two K halves
 # (eight waves, the halves summed through LDS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M,N,K", [(256, 8192, 2048), (1024, 2048, 2048)])
-def test_prefill_two_k_halves(M, N, K):
-    print(f"[prefill-kh] M={M} N={N} K={K}", flush=True)
+def test_prefill_two_k_halves(M, N, K, dtype):
+    print(f"[prefill-kh] M={M} N={N} K={K} {dtype}", flush=True)
     qw, s, z = _weights(N, K, 128, seed=M + 7)
-    x = randn((M, K), seed=M + 8).to(DEV)
+    x = randn((M, K), seed=M + 8, dtype=dtype).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
     _check(out, x, qw, s, z)
     assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
