@@ -5,19 +5,20 @@
 A *step* is one M=1 (decode) pass over the seven linears of one
 Llama-3.2-1B decoder block (q/o 2048x2048, k/v 512x2048, gate/up 8192x2048,
 down 2048x8192; N x K), G=128, bf16 activations, as ONE grouped launch
-(``w4a16_matmul_grouped``).  Steps rotate over 16 distinct seeded weight sets
-(16 x 32.3 MB > the 256 MB Infinity Cache) so weights stream from HBM.
-Inputs are resident in HBM before the timed region; launches are replayed
-from a HIP graph.
+(``w4a16_matmul_grouped``).  Step i uses weight set i % 16: 16 distinct
+seeded sets (16 x 32.3 MB > the 256 MB Infinity Cache) so weights stream from
+HBM.  Inputs are resident in HBM before the timed region.  Exactly --warmup
+untimed steps run, then exactly --steps timed steps as one graph replay
+bracketed by host synchronisation and HIP events on the launch stream.
 
 Printed (last line, JSON): ``value`` = algorithmic HBM bytes of the block
 (sum N*K/2 + 4*N*K/G + 2*K + 2*N = 32,397,312 B) / time per step, in GB/s,
-plus ``roofline`` for the dominant kernel (the grouped decode GEMV, per-launch
-duration from HIP events recorded around each launch inside the graph) and
-``cpu_baseline`` (the CPU oracle, a numpy port of the reference's torch CPU
-dequantize-then-matmul path, timed on a bounded sample).  Extra fields carry
-the per-linear (7-launch) decode block, the split-K M=16 block, the M=2048
-prefill TFLOPS with a hipBLASLt bf16 reference, and the quantize kernel.
+plus ``roofline`` for the dominant kernel (the grouped decode launch, one per
+step) and ``cpu_baseline`` (the reference's torch CPU path -- dequantize to
+bf16, then F.linear -- on all of this host's cores, over the same block).
+Extra fields carry the per-linear (7-launch) decode block, the small-M blocks,
+the M = 128/512/2048 prefill TFLOPS with a hipBLASLt bf16 reference, the
+quantize kernel, HBM read ceilings and the end-to-end Llama-3.2-1B run.
 """
 from __future__ import annotations
 
@@ -58,17 +59,40 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def graph_of(fn, stream):
+def graph_of(fn, stream, eager_warmup: bool = True):
     import torch
 
     g = torch.cuda.CUDAGraph()
     with torch.cuda.stream(stream):
-        fn()  # warm-up outside the graph
+        if eager_warmup:
+            fn()  # warm-up outside the graph
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=stream):
             fn()
     torch.cuda.synchronize()
     return g
+
+
+def time_graph_once(g, stream) -> float:
+    """ms of ONE replay, bracketed by host synchronisation.  A short device-side
+    spin queued just before the start event keeps the GPU busy while the host
+    submits the event and the graph, so that the interval holds the replay's
+    kernels only, not the host's submission latency."""
+    import torch
+
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        try:
+            torch.cuda._sleep(4_000_000)  # ~2 ms of cycles
+        except Exception:  # not available on this stack: the interval includes submission
+            pass
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
 
 
 def time_graph(g, reps: int, stream) -> float:
@@ -87,82 +111,104 @@ def time_graph(g, reps: int, stream) -> float:
     return e0.elapsed_time(e1) / reps
 
 
-def per_launch_ms(launches, stream) -> float | None:
-    """Mean GPU duration of each launch, from event pairs captured around every
-    launch inside one graph (no host gaps between the pair)."""
+def cpu_info() -> dict:
+    """Host CPU model and the cores this process may run on (the CPU timings'
+    thread count)."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "cores": len(os.sched_getaffinity(0))}
+
+
+def _median_s(fn, reps: int) -> float:
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(sorted(ts)[len(ts) // 2])
+
+
+def cpu_baseline(packed, xs, reps: int) -> dict:
+    """The reference's torch CPU path on this host's cores: per linear,
+    ``dequantize_int4_ref(qweight, scales, zeros, bf16)`` then
+    ``F.linear(x, W_hat)`` (int4_triton/quantize.py:128-135,
+    tests/test_kernels.py:56-57), restated as this package's own torch-op
+    functions; ``packed``/``xs`` are the CPU copies of the M=1 block's inputs.
+    Median of ``reps`` passes after one warm-up pass; also the matmul alone on
+    pre-dequantized weights."""
+    import torch
+    import torch.nn.functional as F
+
+    from int4_hip.quantize import dequantize_int4_ref
+
+    info = cpu_info()
+    torch.set_num_threads(info["cores"])
+
+    def block():
+        for (qw, sc, ze), x in zip(packed, xs):
+            F.linear(x, dequantize_int4_ref(qw, sc, ze, torch.bfloat16))
+
+    block()
+    t = _median_s(block, reps)
+    per = {}
+    for (name, _, _), (qw, sc, ze), x in zip(LINEARS, packed, xs):
+        per[name] = round(_median_s(lambda: F.linear(x, dequantize_int4_ref(qw, sc, ze, torch.bfloat16)), 3) * 1e3, 3)
+    w_hat = [dequantize_int4_ref(qw, sc, ze, torch.bfloat16) for qw, sc, ze in packed]
+    t_mm = _median_s(lambda: [F.linear(x, w) for x, w in zip(xs, w_hat)], reps)
+    return {"value": round(block_bytes(1) / t / 1e9, 6), "unit": "GB/s", "cores": info["cores"],
+            "threads": torch.get_num_threads(), "cpu_model": info["cpu_model"], "kind": "port", "impl": "torch",
+            "sample": f"torch CPU path (dequantize_int4_ref to bf16, then F.linear) over the 7-linear block at "
+                      f"M=1, G=128, one weight set, median of {reps} passes ({t * 1e3:.1f} ms per block)",
+            "ms_per_block": round(t * 1e3, 3),
+            "matmul_only_ms_per_block": round(t_mm * 1e3, 3),
+            # configs[0]: the single 2048 x 2048 linear is q_proj's shape
+            "per_linear_ms": per}
+
+
+def cpu_numpy_port(packed_np, xs_bits, reps: int) -> dict:
+    """The numpy oracle (a single-threaded restatement of the same path) over the
+    same block, kept beside the torch figure."""
+    import numpy as np
+
+    from oracle import w4a16_oracle as O
+
+    def block():
+        for (qw, s, z), xb in zip(packed_np, xs_bits):
+            O.w4a16_matmul(xb, "bf16", qw, s, z, accumulate="f32")
+
+    t = _median_s(block, reps)
+    return {"value": round(block_bytes(1) / t / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
+            "impl": "numpy", "ms_per_block": round(t * 1e3, 3),
+            "sample": f"numpy oracle over the M=1 block, median of {reps} passes"}
+
+
+def cpu_quantize_baseline(ws, q_bytes: int, reps: int) -> dict:
+    """The reference's torch quantizer on the CPU (``quantize_int4_ref``,
+    int4_triton/quantize.py:102-117, restated as this package's torch-op
+    function) over the 7 block weights (bf16 CPU tensors), on all cores."""
     import torch
 
-    def ev():
-        try:  # external=True: a real timestamp node inside the captured graph
-            return torch.cuda.Event(enable_timing=True, external=True)
-        except TypeError:
-            return torch.cuda.Event(enable_timing=True)
+    from int4_hip.quantize import quantize_int4_ref
 
-    evs = [(ev(), ev()) for _ in launches]
+    info = cpu_info()
+    torch.set_num_threads(info["cores"])
 
-    def body():
-        for (a, b), fn in zip(evs, launches):
-            a.record(stream)
-            fn()
-            b.record(stream)
+    def block():
+        for w in ws:
+            quantize_int4_ref(w, G)
 
-    try:
-        g = graph_of(body, stream)
-        with torch.cuda.stream(stream):
-            g.replay()
-        torch.cuda.synchronize()
-        ts = [a.elapsed_time(b) for a, b in evs]
-    except Exception as e:  # event nodes not supported in graphs on this stack
-        log(f"per-launch events inside a graph unavailable ({e!r}); using the replay average")
-        return None
-    if min(ts) <= 0:
-        log(f"per-launch events inside a graph gave non-positive durations {ts[:4]}; using the replay average")
-        return None
-    return sum(ts) / len(ts)
-
-
-def cpu_baseline(packed, xs_bits, sample_passes: int) -> dict:
-    """The CPU oracle (numpy port of the reference's torch CPU path:
-    dequantize_int4_ref(..., bf16) then x @ W_hat^T) over the M=1 block.
-    ``packed``: per linear (qweight int32, scales/zeros fp16 bits) as numpy."""
-    import numpy as np
-
-    from oracle import w4a16_oracle as O
-
-    ts, per = [], [[] for _ in packed]
-    for _ in range(sample_passes):
-        t0 = time.perf_counter()
-        for j, ((qw, s, z), xb) in enumerate(zip(packed, xs_bits)):
-            t1 = time.perf_counter()
-            O.w4a16_matmul(xb, "bf16", qw, s, z, accumulate="f32")
-            per[j].append(time.perf_counter() - t1)
-        ts.append(time.perf_counter() - t0)
-    t = float(np.median(ts))
-    return {"value": round(block_bytes(1) / t / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle, dequantize(bf16)+matmul over the 7-linear block at M=1, G=128, "
-                      f"median of {sample_passes} passes ({t * 1e3:.1f} ms per block)",
-            "ms_per_block": round(t * 1e3, 3),
-            # configs[0]: the single 2048 x 2048 linear is q_proj's shape
-            "per_linear_ms": {name: round(float(np.median(p)) * 1e3, 3) for (name, _, _), p in zip(LINEARS, per)}}
-
-
-def cpu_quantize_baseline(w_bits, q_bytes: int, passes: int) -> dict:
-    """The CPU oracle's quantize_int4 (numpy port of the reference's
-    quantize_int4_ref) over the 7 block weights (bf16 bits as numpy)."""
-    import numpy as np
-
-    from oracle import w4a16_oracle as O
-
-    ts = []
-    for _ in range(passes):
-        t0 = time.perf_counter()
-        for w in w_bits:
-            O.quantize_int4(w, "bf16", G)
-        ts.append(time.perf_counter() - t0)
-    t = float(np.median(ts))
-    return {"value": round(q_bytes / t / 1e9, 6), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"numpy oracle quantize_int4 over the 7 block weights (G=128, bf16), "
-                      f"median of {passes} passes ({t * 1e3:.1f} ms per block)",
+    block()
+    t = _median_s(block, reps)
+    return {"value": round(q_bytes / t / 1e9, 6), "unit": "GB/s", "cores": info["cores"],
+            "threads": torch.get_num_threads(), "cpu_model": info["cpu_model"], "kind": "port", "impl": "torch",
+            "sample": f"torch quantize_int4_ref over the 7 block weights (G=128, bf16), "
+                      f"median of {reps} passes ({t * 1e3:.1f} ms per block)",
             "ms_per_block": round(t * 1e3, 3)}
 
 
@@ -188,10 +234,12 @@ def device_copy_gbps(dev, stream, nbytes: int = 1 << 30, reps: int = 10) -> floa
 
 
 def hbm_read_ceiling(dev, stream, block_bytes_: int, nsets: int) -> dict | None:
-    """Measured read ceilings (csrc/bench/read_probe.hip, a kernel that only
-    reads): one long stream over 1 GiB, and one launch per set over `nsets`
-    rotated buffers of the decode block's size, replayed from a graph -- the
-    practical bound for a single launch that moves the block's bytes."""
+    """Measured read ceilings (csrc/bench/read_probe.hip, kernels that only
+    read): one long stream over 1 GiB, and the best single launch over the
+    decode block's bytes -- one 1024-thread workgroup per CU, each reading a
+    contiguous slice with every load in flight -- over ``nsets`` rotated
+    buffers from a graph (default and non-temporal loads; also the older
+    grid-stride launch of 512 workgroups)."""
     import ctypes
 
     import torch
@@ -204,13 +252,22 @@ def hbm_read_ceiling(dev, stream, block_bytes_: int, nsets: int) -> dict | None:
     fn = lib.w4bench_read
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    fs = lib.w4bench_read_slices
+    fs.restype = ctypes.c_int
+    fs.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     sink = torch.zeros(16, dtype=torch.int32, device=dev)
     raw = stream.cuda_stream
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
 
     def launch(buf, nbytes, grid, block):
         rc = fn(buf.data_ptr(), nbytes, grid, block, sink.data_ptr(), raw)
         if rc != 0:
             raise RuntimeError(f"w4bench_read failed ({rc})")
+
+    def slices(buf, nbytes, nt):
+        rc = fs(buf.data_ptr(), nbytes, cus, nt, sink.data_ptr(), raw)
+        if rc != 0:
+            raise RuntimeError(f"w4bench_read_slices failed ({rc})")
 
     big = torch.ones(1 << 28, dtype=torch.int32, device=dev)  # 1 GiB
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -226,14 +283,25 @@ def hbm_read_ceiling(dev, stream, block_bytes_: int, nsets: int) -> dict | None:
     del big
     n16 = block_bytes_ // 16 * 16
     bufs = [torch.ones(n16 // 4, dtype=torch.int32, device=dev) for _ in range(nsets)]
-    g = graph_of(lambda: [launch(b, n16, 512, 1024) for b in bufs], stream)
-    time_graph(g, 3, stream)
-    us = time_graph(g, 10, stream) / nsets * 1e3
-    del g, bufs
-    return {"stream_1gib_gbps": round(stream_gbps, 1), "single_launch_block_bytes_us": round(us, 3),
-            "single_launch_block_bytes_gbps": round(n16 / (us * 1e-6) / 1e9, 1),
-            "note": "read-only kernel, 16-byte loads; stream: 2048 x 256 threads over 1 GiB; single launch: "
-                    f"512 x 1024 threads over {n16} B, {nsets} rotated buffers, graph replay"}
+    out = {"stream_1gib_gbps": round(stream_gbps, 1)}
+    for key, body in (("slices", lambda: [slices(b, n16, 0) for b in bufs]),
+                      ("slices_nt", lambda: [slices(b, n16, 1) for b in bufs]),
+                      ("grid_stride", lambda: [launch(b, n16, 512, 1024) for b in bufs])):
+        g = graph_of(body, stream)
+        time_graph(g, 3, stream)
+        us = time_graph(g, 10, stream) / nsets * 1e3
+        del g
+        out[f"single_launch_{key}_us"] = round(us, 3)
+        out[f"single_launch_{key}_gbps"] = round(n16 / (us * 1e-6) / 1e9, 1)
+    del bufs
+    best = min(out["single_launch_slices_us"], out["single_launch_slices_nt_us"], out["single_launch_grid_stride_us"])
+    out["single_launch_block_bytes_us"] = best
+    out["single_launch_block_bytes_gbps"] = round(n16 / (best * 1e-6) / 1e9, 1)
+    out["note"] = (f"read-only kernels, 16-byte loads, {n16} B per launch over {nsets} rotated buffers, graph "
+                   f"replay; slices: {cus} workgroups x 1024 threads, one contiguous slice each, all loads of a "
+                   "thread issued before use (default / non-temporal loads); grid_stride: 512 x 1024 threads; "
+                   "stream: 2048 x 256 threads over 1 GiB")
+    return out
 
 
 PROFILE = ROOT / "profiles" / "dec_kernel_one_decode_block_m1.md"
@@ -317,7 +385,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--sets", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-passes", type=int, default=30)
+    ap.add_argument("--cpu-reps", type=int, default=7, help="timed passes of each CPU baseline (median)")
+    ap.add_argument("--cpu-numpy", action="store_true", help="also time the single-core numpy oracle")
     ap.add_argument("--only", default="all",
                     help="comma list of sections to run: decode, perlinear, splitk, prefill, quantize, llama "
                          "(profiling runs use one section; the JSON line needs 'decode')")
@@ -387,21 +456,30 @@ def main() -> int:
     def grouped(i):
         return lambda: int4_hip.w4a16_matmul_grouped(xs1[i], packed[i], out=ys1[i])
 
-    steps = max(nsets, (args.steps + nsets - 1) // nsets * nsets)
-    warm = max(1, args.warmup // nsets)
+    steps, warm = args.steps, args.warmup
     bytes1 = block_bytes(1)
     ms_per_step = kern_ms = value = achieved = None
     kern_ms_src = None
     if "decode" in only:
-        g_main = graph_of(lambda: [grouped(i)() for i in range(nsets)], stream)
-        time_graph(g_main, warm, stream)
-        ms_rot = time_graph(g_main, steps // nsets, stream)
-        ms_per_step = ms_rot / nsets
+        # exactly `warm` untimed steps, then exactly `steps` timed ones: step i
+        # is one grouped launch over weight set i % nsets.  Both graphs are
+        # captured without an eager call (the M = 1 decode launch needs no
+        # workspace), so no other step runs.
+        def run(n):
+            return lambda: [grouped(i % nsets)() for i in range(n)]
+
+        g_main = graph_of(run(steps), stream, eager_warmup=False)
+        if warm > 0:
+            g_warm = graph_of(run(warm), stream, eager_warmup=False)
+            with torch.cuda.stream(stream):
+                g_warm.replay()
+            del g_warm
+        ms_run = time_graph_once(g_main, stream)
+        ms_per_step = ms_run / steps
         value = bytes1 / (ms_per_step * 1e-3) / 1e9
-        kern_ms = per_launch_ms([grouped(i) for i in range(nsets)], stream)
-        kern_ms_src = "hip-events-around-each-launch-in-graph"
-        if kern_ms is None:
-            kern_ms, kern_ms_src = ms_per_step, "graph-replay-average (16 launches per replay)"
+        # one kernel per step: the roofline kernel's average duration is the
+        # timed region over its launches (HIP events on the launch stream)
+        kern_ms, kern_ms_src = ms_per_step, "hip-events-on-launch-stream-over-the-timed-steps"
         achieved = bytes1 / (kern_ms * 1e-3) / 1e9
         del g_main
 
@@ -553,14 +631,18 @@ def main() -> int:
         torch.cuda.synchronize()
 
     # ------------------------------------------------- CPU baseline (rank 0, N=1)
-    cpu = cpu_q = None
+    cpu = cpu_q = cpu_np = None
     if not args.no_cpu:
         def bits(t):
             return t.contiguous().view(torch.int16).numpy().view(np.uint16)
-        packed0 = [(qw.cpu().numpy(), bits(s.cpu()), bits(z.cpu())) for qw, s, z in packed[0]]
-        cpu = cpu_baseline(packed0, [bits(x.cpu()) for x in xs1[0]], args.cpu_passes)
+        packed0 = [tuple(t.cpu() for t in p) for p in packed[0]]
+        xs0 = [x.cpu() for x in xs1[0]]
+        cpu = cpu_baseline(packed0, xs0, args.cpu_reps)
+        if args.cpu_numpy:
+            cpu_np = cpu_numpy_port([(qw.numpy(), bits(sc), bits(ze)) for qw, sc, ze in packed0],
+                                    [bits(x) for x in xs0], 3)
         if "quantize" in only:
-            cpu_q = cpu_quantize_baseline([bits(w) for w in w16_host], q_bytes, 3)
+            cpu_q = cpu_quantize_baseline(w16_host, q_bytes, args.cpu_reps)
     copy_gbps = device_copy_gbps(dev, stream) if "decode" in only else None
     read_ceiling = hbm_read_ceiling(dev, stream, bytes1, nsets) if "decode" in only else None
 
@@ -571,7 +653,7 @@ def main() -> int:
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": warm * nsets,
+        "warmup": warm,
         "ms_per_step": round(ms_per_step, 6) if ms_per_step is not None else None,
         "us_per_block": round(ms_per_step * 1e3, 3) if ms_per_step is not None else None,
         "higher_is_better": True,
@@ -591,6 +673,7 @@ def main() -> int:
             "kernel": "w4::" + ROOFLINE_KERNEL, "kernel_us": round(kern_ms * 1e3, 3),
             "kernel_time_source": kern_ms_src},
         "cpu_baseline": cpu,
+        "cpu_baseline_numpy_port": cpu_np,
         "decode_m1_per_linear_us": {k: round(v, 3) for k, v in per_lin.items()},
         "decode_m1_per_linear_gbps": {name: round(lin_bytes(N, K) / (per_lin[name] * 1e-6) / 1e9, 1)
                                       for name, N, K in LINEARS if name in per_lin},

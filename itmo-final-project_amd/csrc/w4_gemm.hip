@@ -49,7 +49,13 @@ extern "C" size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int gro
   if (M > kSmallM) {
     scratch = w4_prefill_workspace_bytes(M, N, K);
   } else if (M <= kDecodeM) {
-    scratch = w4_gemv_workspace_bytes(M, N, K, group_size);
+    // dense rows take the decode / gemv kernels, strided or unaligned rows the
+    // skinny split-K kernel (whose split count may differ): room for either
+    const size_t a = w4_gemv_workspace_bytes(M, N, K, group_size);
+    const size_t b = w4_skinny_workspace_bytes(M, N, K, (N % 4) == 0);
+    const size_t c = w4_skinny_workspace_bytes(M, N, K, false);
+    scratch = a > b ? a : b;
+    scratch = scratch > c ? scratch : c;
   } else {
     // the pipelined MFMA kernel or, for strided / unaligned / K % 64 != 0
     // operands, the skinny kernel: room for either
@@ -190,3 +196,4 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
                 "split problems exceed the counter area");
   return lrc;
 }
+

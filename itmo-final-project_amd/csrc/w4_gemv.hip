@@ -529,7 +529,10 @@ int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, 
     const int rc = w4_decode_launch(&q, &sxm, &ldy, 1, x_dtype, M, st);
     if (rc != W4_ERR_UNSUPPORTED) return rc;
   }
-  if (M == 1 && sxk == 1 && ldy == N && counters != nullptr) {
+  // M == 1: the grouped kernel with its in-kernel split fixup.  Without a
+  // workspace it refuses (W4_ERR_WORKSPACE, nothing launched) rather than
+  // taking another route, so the summation order is a function of the shape.
+  if (M == 1 && sxk == 1 && ldy == N) {
     w4a16_problem q{x, qw, sc, ze, y, N, K, G, 0};
     const int rc = w4_gemv_grouped_launch(&q, 1, x_dtype, 1, counters, ws, ws_bytes, st);
     if (rc != W4_ERR_UNSUPPORTED) return rc;

@@ -19,8 +19,10 @@ bit-identical from run to run and process to process (the reference picks its
 tiles by timing, gemm.py:161-168).  Every call launches on the caller's
 current stream and never synchronizes.  The split-K workspace is one
 persistent zero-initialised buffer per (device, stream), allocated on the first
-call and never freed (the kernels leave its counters zero), so calls made after
-a warm-up call can be captured in a CUDA/HIP graph.
+call and never freed (the kernels leave its counters zero); a call captured on a
+stream that has none runs without one when its route needs none, else with a
+graph-private buffer (see ``_with_workspace``), so graphs can be captured with
+or without a warm-up call on the capture stream.
 """
 from __future__ import annotations
 
@@ -50,8 +52,10 @@ _WS_ALL: list = []
 _WS_LOCK = threading.Lock()
 
 
-def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    """Persistent zero-initialised split-K workspace, one per (device, stream).
+def _stream_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
+    """The persistent zero-initialised workspace of (device, stream), grown to
+    ``nbytes`` outside graph capture; None if it is missing or too small while
+    the stream is capturing.
 
     The kernels leave its counter area zero, so it is reused as is; buffers are
     never freed, so graphs that captured one keep a valid pointer.  Calls on
@@ -62,12 +66,38 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
         if ws is not None and ws.numel() >= nbytes:
             return ws
         if torch.cuda.is_current_stream_capturing():
-            raise RuntimeError("int4_hip: run this call once before graph capture "
-                               "(its split-K workspace is allocated on the first call)")
+            return None
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WS_ALL.append(ws)
         _WS[key] = ws
         return ws
+
+
+def _with_workspace(device: torch.device, stream: int, nbytes: int, launch) -> int:
+    """``launch(ptr, nbytes)`` with a workspace of at least ``nbytes`` (``nbytes``
+    is the library's size query, an upper bound over every route the call may
+    take).
+
+    A graph may be captured on a stream that never ran an eager call (torch's
+    own capture stream, as ``torch.cuda.graph(g)`` without a stream and
+    ``triton.testing.do_bench_cudagraph`` use).  There the call first runs
+    without a workspace: most shapes need none, and the library refuses with
+    W4_ERR_WORKSPACE before launching anything when the route it takes does.
+    Only then is a buffer taken from the graph's private memory, zeroed by a
+    fill kernel that the graph records ahead of the product (so every replay
+    starts from zero counters) and kept for the life of the process."""
+    if nbytes == 0:
+        return launch(None, 0)
+    ws = _stream_workspace(device, stream, nbytes)
+    if ws is not None:
+        return launch(ws.data_ptr(), ws.numel())
+    rc = launch(None, 0)
+    if rc != _lib.ERR_WORKSPACE:
+        return rc
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    with _WS_LOCK:
+        _WS_ALL.append(ws)
+    return launch(ws.data_ptr(), ws.numel())
 
 
 _WS_BYTES: dict = {}
@@ -87,13 +117,10 @@ def _gemm_call(lib, x2, dt, M, N, K, qweight, scales, zeros, G, y, device):
     # torch.cuda.current_stream(); the library reads the current device (for
     # its CU count), which the caller has made the tensors' device
     stream = torch._C._cuda_getCurrentRawStream(device.index)
-    nb = _ws_bytes(lib, M, N, K, G)
-    ws = _workspace(device, stream, nb) if nb else None
-    return lib.w4a16_gemm(
+    return _with_workspace(device, stream, _ws_bytes(lib, M, N, K, G), lambda ws, nb: lib.w4a16_gemm(
         x2.data_ptr(), dt, M, N, K, x2.stride(0), x2.stride(1),
         qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(), G,
-        y.data_ptr(), N, ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0,
-        stream)
+        y.data_ptr(), N, ws, nb, stream))
 
 
 def w4a16_matmul(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor) -> torch.Tensor:
@@ -169,9 +196,8 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
     def call():
         stream = torch._C._cuda_getCurrentRawStream(dev.index)
         nbytes = lib.w4a16_grouped_workspace_bytes(probs, len(xs), M)
-        ws = _workspace(dev, stream, nbytes) if nbytes else None
-        return lib.w4a16_gemm_grouped(probs, len(xs), _XDT[dt], M, ws.data_ptr() if ws is not None else None,
-                                      ws.numel() if ws is not None else 0, stream)
+        return _with_workspace(dev, stream, nbytes, lambda ws, nb: lib.w4a16_gemm_grouped(
+            probs, len(xs), _XDT[dt], M, ws, nb, stream))
 
     if torch._C._cuda_getDevice() == dev.index:
         rc = call()

@@ -1,78 +1,17 @@
-"""GPU parity of the W4A16 GEMM regimes against the CPU oracle.
-
-Tolerances (stated per the task's floating-point bar):
-* ``max |y - ref| <= 1e-2 * max |ref|`` with ref = x @ W_hat^T in float64 and
-  W_hat rounded once to the activation dtype (the reference's own kernels
-  round W_hat that way, int4_triton/gemm.py:139,211) -- the north-star bound;
-* elementwise ``|y - ref| <= u_out * |ref| + 2**-20 * (|x| @ |W_hat|^T)``:
-  one rounding of the output (u_out = 2**-8 bf16, 2**-11 fp16) plus fp32
-  accumulation error;
-* the reference's own check against the unrounded fp32 W_hat
-  (tests/test_kernels.py:60): rtol 2e-2, atol 2e-2 * max |ref|.
-
-The decode regime (M <= 16, group size >= 32, dense activation rows) applies
-scales and zero points after the matrix-core sums, so it multiplies by the
-exact fp32 W_hat instead of W_hat rounded to the activation dtype.  Its
-elementwise check is against ref = x @ W_hat_fp32^T with
-``|y - ref| <= u_out * |ref| + c * sum_k |x_k| s_{g(k)}``: the fp32 rounding of
-the per-group sums of x_k * (OFF + QS q_k), whose terms are at most 143 |x_k|
-(bf16: 128 + q) or 31 |x_k| (fp16: (1024 + 64 q) / 64), c = 2**-10 (bf16),
-2**-12 (fp16).  A wrong zero point, scale, nibble or group is off by about
-s * |sum_g x|, orders of magnitude above that slack.
-"""
+"""GPU parity of the W4A16 GEMM regimes against the CPU oracle, with the
+tolerances stated in tests/_checks.py (max relative error <= 1e-2, an
+elementwise bound from the output rounding and fp32 accumulation, and the
+reference's own rtol/atol check), plus bit-identical repeat runs, graph
+capture and workspace handling."""
 import numpy as np
 import pytest
 import torch
 
 import int4_hip
-from oracle import w4a16_oracle as O
-from _synth import bits_of, dtype_name, randn
+from _checks import DEV, _check, _decode, _weights
+from _synth import randn
 
 pytestmark = pytest.mark.gpu
-DEV = "cuda"
-U_OUT = {torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
-
-
-def _decode(M: int, G: int, N: int = 0, K: int = 1 << 30) -> bool:
-    """True when w4a16_matmul takes the factored decode kernel (dense, aligned
-    rows): M <= 16, or M <= 32 with 64-column tiles (N % 4 == 0, K <= 4096,
-    group >= 64)."""
-    return G >= 32 and (M <= 16 or (M <= 32 and G >= 64 and N % 4 == 0 and K <= 4096))
-
-
-def _check(out: torch.Tensor, x: torch.Tensor, qw, s, z, ref_unrounded: bool = True, exact_w: bool = False):
-    xd = dtype_name(x.dtype)
-    x2 = x.reshape(-1, x.shape[-1])
-    qn, sn, zn = qw.cpu().numpy(), bits_of(s), bits_of(z)
-    xa = np.abs(O.half_bits_to_f32(bits_of(x2), xd).astype(np.float64))
-    if exact_w:
-        ref = O.w4a16_matmul(bits_of(x2), xd, qn, sn, zn, w_hat_dtype="fp32")  # float64
-        G = x2.shape[1] // sn.shape[0]
-        s_abs = np.abs(O.half_bits_to_f32(sn, "fp16").astype(np.float64))
-        slack = (2.0**-10 if x.dtype == torch.bfloat16 else 2.0**-12) * (xa @ np.repeat(s_abs, G, axis=0))
-    else:
-        ref = O.w4a16_matmul(bits_of(x2), xd, qn, sn, zn)               # float64
-        w_hat = O.dequantize_int4(qn, sn, zn, xd).astype(np.float64)
-        slack = 2.0**-20 * (xa @ np.abs(w_hat).T)
-    y = out.reshape(-1, out.shape[-1]).float().cpu().numpy().astype(np.float64)
-    assert y.shape == ref.shape
-    err = np.abs(y - ref)
-    scale = max(np.abs(ref).max(), 1e-30)
-    assert err.max() <= 1e-2 * scale, f"max rel err {err.max() / scale:.3e}"
-    bound = U_OUT[x.dtype] * np.abs(ref) + slack + 1e-30
-    bad = err > bound
-    assert not bad.any(), f"{int(bad.sum())} elements outside the elementwise bound, first {np.argwhere(bad)[0]}"
-    if ref_unrounded:
-        ref32 = O.w4a16_matmul(bits_of(x2), xd, qn, sn, zn, w_hat_dtype="fp32")
-        torch.testing.assert_close(torch.from_numpy(y), torch.from_numpy(ref32), rtol=2e-2,
-                                   atol=2e-2 * np.abs(ref32).max())
-
-
-def _weights(N, K, G, seed, wdtype=torch.bfloat16):
-    w = randn((N, K), seed=seed, sigma=0.02, dtype=wdtype).to(DEV)
-    return int4_hip.quantize_int4(w, G)
-
-
 # int4_triton tests/test_kernels.py:47-60 (M x shape x dtype grid)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("M", [1, 7, 24, 128, 512, 2048])
@@ -87,10 +26,22 @@ def test_w4a16_matmul(M, NK, dtype):
     _check(out, x, qw, s, z, exact_w=_decode(M, 128, N, K))
 
 
-# split-K regime over the block's shapes and the three group sizes
+def _poison_workspace():
+    """NaN into the scratch part of the current stream's persistent workspace
+    (past the counter area, which must stay zero), so that a kernel reading a
+    partial it did not write this call shows up as NaN or a changed bit."""
+    from int4_hip import gemm as _gemm
+    ws = _gemm._WS.get((torch.cuda.current_device(), torch.cuda.current_stream().cuda_stream))
+    if ws is not None:
+        scratch = ws[65536:]
+        scratch[: scratch.numel() // 4 * 4].view(torch.float32).fill_(float("nan"))
+
+
+# split-K regime over the block's shapes (all four distinct N x K of
+# bench_gemm.py:18-26) and the three group sizes
 @pytest.mark.parametrize("G", [128, 64, 32])
 @pytest.mark.parametrize("M", [2, 4, 8, 16, 24, 32, 64])
-@pytest.mark.parametrize("NK", [(2048, 2048), (512, 2048), (2048, 8192)])
+@pytest.mark.parametrize("NK", [(2048, 2048), (512, 2048), (8192, 2048), (2048, 8192)])
 def test_split_k_regime(M, NK, G):
     N, K = NK
     print(f"[split-k] M={M} N={N} K={K} G={G}", flush=True)
@@ -98,10 +49,9 @@ def test_split_k_regime(M, NK, G):
     x = randn((M, K), seed=100 + M).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
     _check(out, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, G, N, K))
-    # bit-identical repeat runs, with the workspace poisoned in between
-    junk = torch.full((64 << 20,), float("nan"), device=DEV)
-    del junk
+    # bit-identical repeat runs, with the workspace's scratch poisoned in between
     for _ in range(2):
+        _poison_workspace()
         again = int4_hip.w4a16_matmul(x, qw, s, z)
         assert torch.equal(again.view(torch.int16), out.view(torch.int16))
 
@@ -316,3 +266,75 @@ def test_grouped_shared_activation(M, K, Ns, G):
     mixed = int4_hip.w4a16_matmul_grouped(xs, ws)
     for xi, (qw, s, z), y in zip(xs, ws, mixed):
         _check(y, xi, qw, s, z, ref_unrounded=not ew, exact_w=ew)
+
+
+def _replays_match(g, out, eager, reps=3):
+    """Replay a captured graph several times, with eager work and host
+    synchronisation between replays; every replay must equal the eager bits."""
+    for _ in range(reps):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16))
+        torch.randn(1 << 16, device=DEV).sum().item()
+
+
+# capture on torch's own capture stream after a warm-up on another stream, as
+# eval_llama.py:145-161 (decode step) and triton's do_bench_cudagraph
+# (bench_gemm.py:33-36) do: M = 1 decode shapes whose size query is nonzero,
+# and split-K shapes that need the workspace
+@pytest.mark.parametrize("M,N,K,G", [(1, 2048, 8192, 128), (1, 2048, 2048, 128), (1, 300, 2048, 16),
+                                     (40, 2048, 8192, 128), (64, 8192, 2048, 128), (128, 512, 2048, 128)])
+def test_capture_without_warmup_on_capture_stream(M, N, K, G):
+    print(f"[capture] M={M} N={N} K={K} G={G}", flush=True)
+    qw, s, z = _weights(N, K, G, seed=M + N + G)
+    x = randn((M, K), seed=M + 3).to(DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = int4_hip.w4a16_matmul(x, qw, s, z)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    _check(eager, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, G, N, K))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):  # no stream: torch's default capture stream
+        out = int4_hip.w4a16_matmul(x, qw, s, z)
+    _replays_match(g, out, eager)
+
+
+def test_capture_grouped_without_warmup():
+    shapes = [(2048, 2048), (512, 2048), (512, 2048), (2048, 8192)]
+    ws = [_weights(N, K, 32 if i == 3 else 128, seed=500 + i) for i, (N, K) in enumerate(shapes)]
+    for M in (1, 40):
+        print(f"[capture grouped] M={M}", flush=True)
+        xs = [randn((M, K), seed=510 + i).to(DEV) for i, (N, K) in enumerate(shapes)]
+        eager = int4_hip.w4a16_matmul_grouped(xs, ws)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs = int4_hip.w4a16_matmul_grouped(xs, ws)
+        for _ in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            for a, b in zip(outs, eager):
+                assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+            torch.randn(1 << 16, device=DEV).sum().item()
+
+
+# strided activation rows (row stride not a multiple of 8) take the skinny
+# split-K kernel even at M <= 16; a fresh stream sizes its workspace from the
+# size query, which must cover that route too
+@pytest.mark.parametrize("M,N,K", [(16, 3072, 14336), (5, 2048, 8192)])
+def test_strided_rows_workspace_on_new_stream(M, N, K):
+    print(f"[strided ws] M={M} N={N} K={K}", flush=True)
+    qw, s, z = _weights(N, K, 128, seed=N + 1)
+    big = randn((M, K + 4), seed=K).to(DEV)
+    x = big[:, :K]
+    assert x.stride(0) % 8 != 0
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        out = int4_hip.w4a16_matmul(x, qw, s, z)
+        again = int4_hip.w4a16_matmul(x, qw, s, z)
+    torch.cuda.synchronize()
+    _check(out, x, qw, s, z, ref_unrounded=False)
+    assert torch.equal(again.view(torch.int16), out.view(torch.int16))
