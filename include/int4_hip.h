@@ -164,6 +164,31 @@ size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, i
 int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
                        void* workspace, size_t workspace_bytes, void* stream);
 
+/* Scratch memory of w4a16_gemm_noalloc, per GPU: the counter area plus 32 MiB
+ * of fp32 partial sums. */
+#define W4_NOALLOC_SCRATCH_BYTES (W4_WORKSPACE_COUNTER_BYTES + (32u << 20))
+
+/*
+ * w4a16_gemm without a workspace argument and without any allocation: the
+ * same validation, launch regimes, kernels and output bits as w4a16_gemm, with
+ * the split-K scratch taken from a fixed array inside the library (one per
+ * GPU, W4_NOALLOC_SCRATCH_BYTES, held until the process ends).  Problems whose
+ * w4a16_workspace_bytes exceeds that size are rejected with W4_ERR_WORKSPACE
+ * before anything is launched.  It calls no hipMalloc/hipFree and no
+ * allocating library routine; it may enqueue one small fill kernel that
+ * zeroes the counter area before the product.
+ * All calls on one GPU share its scratch array: calls that may overlap in time
+ * on one GPU (on different streams, or from several threads without ordering)
+ * race on it and must not be issued.  Calls ordered on one stream are safe.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid allocation).
+ */
+int w4a16_gemm_noalloc(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                       int64_t stride_xm, int64_t stride_xk,
+                       const int32_t* qweight, const uint16_t* scales, const uint16_t* zeros,
+                       int group_size, void* y, int64_t ldy, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

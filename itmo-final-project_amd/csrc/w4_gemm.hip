@@ -2,6 +2,8 @@
 // of int4_triton/gemm.py:234-309).
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "w4_common.hpp"
 
 using namespace w4host;
@@ -197,3 +199,83 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
   return lrc;
 }
 
+// ------------------------------------------------------------------------
+// w4a16_gemm_noalloc: w4a16_gemm with the library's own scratch memory.
+//
+// The workspace lives in this file-scope device array: one copy per GPU,
+// allocated by the runtime when the library's code object is loaded there and
+// held until the process ends.  Host code never passes `scratch` itself (on
+// the host the name is only a stand-in for the device symbol): its device
+// address is looked up once per device with hipGetSymbolAddress and cached.
+static __device__ __align__(256) unsigned char scratch[W4_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxNoAllocDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxNoAllocDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call made with that device current).
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(W4_ERR_LAUNCH, "w4a16_gemm_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxNoAllocDevices)
+    return fail(W4_ERR_UNSUPPORTED, "w4a16_gemm_noalloc: device index %d beyond %d", dev, kMaxNoAllocDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(W4_ERR_LAUNCH, "w4a16_gemm_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return W4_OK;
+}
+
+// Zeroes n32 words (n32 % 4 == 0) with 16-byte vector stores.
+__global__ void clear_words_kernel(uint32_t* __restrict__ p, int n32) {
+  const int i = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i < n32) *reinterpret_cast<w4::u32x4*>(p + i) = w4::u32x4{0u, 0u, 0u, 0u};
+}
+
+}  // namespace
+
+extern "C" int w4a16_gemm_noalloc(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                                  int64_t stride_xm, int64_t stride_xk, const int32_t* qweight,
+                                  const uint16_t* scales, const uint16_t* zeros, int group_size, void* y,
+                                  int64_t ldy, void* stream) {
+  clear_error();
+  // the same validation as w4a16_gemm, before the scratch size is asked for
+  if (x_dtype != W4_DTYPE_BF16 && x_dtype != W4_DTYPE_FP16)
+    return fail(W4_ERR_INVALID, "w4a16_gemm_noalloc: x dtype must be bf16 or fp16 (got code %d)", x_dtype);
+  if (M < 0 || N < 0 || K < 8 || K % 8 != 0 || group_size < 8 || !is_pow2(group_size) || K % group_size != 0)
+    return fail(W4_ERR_INVALID, "w4a16_gemm_noalloc: bad shape M=%lld N=%lld K=%lld group_size=%d",
+                (long long)M, (long long)N, (long long)K, group_size);
+  if (M == 0 || N == 0) return W4_OK;
+  const size_t need = w4a16_workspace_bytes(M, N, K, group_size);
+  if (need > (size_t)W4_NOALLOC_SCRATCH_BYTES)
+    return fail(W4_ERR_WORKSPACE,
+                "w4a16_gemm_noalloc: this problem needs %zu bytes of scratch, above the library's fixed %zu "
+                "(M=%lld N=%lld K=%lld); use w4a16_gemm with a workspace",
+                need, (size_t)W4_NOALLOC_SCRATCH_BYTES, (long long)M, (long long)N, (long long)K);
+  void* ws = nullptr;
+  int rc = noalloc_scratch(&ws);
+  if (rc != W4_OK) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (need > 0) {
+    // the arrival counters must start at zero; the previous call on this GPU
+    // left them zero, but a fill kernel (not a memset node, so that the call
+    // can sit inside a captured graph) makes that hold whatever ran before
+    const int n32 = W4_WORKSPACE_COUNTER_BYTES / 4;
+    hipLaunchKernelGGL(clear_words_kernel, dim3((unsigned)((n32 / 4 + 255) / 256)), dim3(256), 0, st,
+                       static_cast<uint32_t*>(ws), n32);
+    rc = check_launch("w4a16_gemm_noalloc (counter clear)");
+    if (rc != W4_OK) return rc;
+  }
+  return w4a16_gemm(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, group_size, y, ldy, ws,
+                    (size_t)W4_NOALLOC_SCRATCH_BYTES, stream);
+}

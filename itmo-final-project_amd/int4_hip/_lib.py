@@ -23,6 +23,8 @@ ERR_UNSUPPORTED = 2
 ERR_WORKSPACE = 3
 ERR_LAUNCH = 4
 MAX_GROUPED = 8
+WORKSPACE_COUNTER_BYTES = 65536
+NOALLOC_SCRATCH_BYTES = WORKSPACE_COUNTER_BYTES + (32 << 20)
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -57,6 +59,8 @@ SIGNATURES = {
                             _c_vp, _c_i64, _c_vp, _c_sz, _c_vp]),
     "w4a16_grouped_workspace_bytes": (_c_sz, [ctypes.POINTER(Problem), _c_int, _c_i64]),
     "w4a16_gemm_grouped": (_c_int, [ctypes.POINTER(Problem), _c_int, _c_int, _c_i64, _c_vp, _c_sz, _c_vp]),
+    "w4a16_gemm_noalloc": (_c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp,
+                                    _c_int, _c_vp, _c_i64, _c_vp]),
 }
 
 _lock = threading.Lock()
