@@ -56,6 +56,13 @@ struct DecArgs {
   int gshift;  // log2(group size), >= 5
   int vec;     // generic path: columns per lane, 4, 2 or 1
   int cfg;     // M == 1: kCfg* tiling of dec_kernel_one
+  // M == 1, dec_kernel_one: K parts per column tile (a power of two).  1: the
+  // workgroup covers all of K and writes y.  > 1: workgroup t covers part
+  // t % ksplit of column tile t / ksplit; the parts of a column meet pairwise
+  // in a fixed binary tree of 64-bit words `pair` [tile][ksplit - 1][TW]
+  // (zero on entry and left zero), see dec_split_finish.
+  int ksplit;
+  unsigned long long* pair;
 };
 
 // M == 1 tilings (dec_kernel_one)
@@ -492,6 +499,70 @@ constexpr int one_lds(int mr) {
   return one_red_offset(mr) + (mr >= 8 ? 0 : kOneWaves * mr * 128 * (int)sizeof(float));
 }
 
+// K-split tile (M == 1): wave 0 sums the per-wave partials of the tile's 128
+// columns (two per lane, same fixed order as above) and publishes them as fp32
+// partials with device-coherent stores (sc1: no device-wide cache write-back
+// is needed to make them visible); once they have completed it bumps the
+// tile's arrival counter (a relaxed device-scope atomic).  The last of the
+// tile's ks workgroups reads all parts back with device-coherent loads, sums
+// them in part order and writes y, then leaves the counter at zero.  Every
+// output bit is a function of the inputs only.
+constexpr int kMaxKSplit = 8;  // K parts of one M == 1 column tile
+
+// K-split tile (M == 1): wave 0 sums the per-wave partials of each of the
+// tile's columns (one or two per lane, the fixed wave order of the unsplit
+// reduction), then the parts of a column combine pairwise up a fixed binary
+// tree (parts 2i and 2i+1 first, then those pairs, ...).  Each tree node is a
+// 64-bit word, zero when free: a part arriving at a node swaps in
+// (1 << 32 | bits of its value) with one compare-and-swap; if the word was
+// zero it leaves, otherwise it received its sibling's value, adds it, frees
+// the word and climbs.  IEEE addition is commutative (a + b and b + a give the
+// same bits), so whichever sibling arrives second computes the same sum: the
+// result is a function of the inputs only, and the last part's critical path
+// is one atomic round trip per tree level, with no cache flush and no
+// partial-sum buffer (the value travels in the atomic).
+// red: the per-wave partial tiles of the cross-wave reduction, wave w's
+// column nl at red[w * RSTR + nl]
+template <int DT, int TW, int RSTR>
+__device__ __forceinline__ void dec_split_finish(const DecArgs& a, const float* red, int ct, int kp, int ks, int n0,
+                                                 int lane) {
+  typedef DecNum<DT> Num;
+  static_assert(TW % 64 == 0, "split tiles: whole lanes per column");
+  constexpr int C = TW / 64;
+  unsigned long long* words = a.pair + (int64_t)ct * (ks - 1) * TW;
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int nl = c * 64 + lane;
+    float pv[kOneWaves];
+#pragma unroll
+    for (int w = 0; w < kOneWaves; ++w) pv[w] = red[w * RSTR + nl];
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kOneWaves; ++w) v += pv[w];
+    v *= 1.0f / Num::QS;
+    bool live = true;
+    int base = 0;
+    for (int width = ks >> 1, node = kp >> 1; width >= 1; base += width, width >>= 1, node >>= 1) {
+      if (live) {
+        unsigned long long* wd = words + (int64_t)(base + node) * TW + nl;
+        unsigned long long seen = 0ull;
+        const unsigned long long mine = (1ull << 32) | (unsigned long long)__builtin_bit_cast(uint32_t, v);
+        if (__hip_atomic_compare_exchange_strong(wd, &seen, mine, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) {
+          live = false;  // first of the pair: the sibling finishes
+        } else {
+          v += __builtin_bit_cast(float, (uint32_t)seen);
+          __hip_atomic_store(wd, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    if (live && n0 + nl < a.N) {
+      if (v != v) v = __builtin_bit_cast(float, 0x7FC00000u);  // one NaN pattern whatever the order
+      a.y[n0 + nl] = float_to_act_bits<DT>(v);
+    }
+  }
+}
+
 template <int DT, int TW, int GSI, int NL, int D, int MR>
 __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t* lds) {
   typedef typename Act<DT>::frag F;
@@ -546,11 +617,16 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     part = lane >= 40 ? 1 : 0;
   }
   const int N = a.N, K = a.K, M = MR == 1 ? 1 : a.M;
-  const int n0 = tile * TW;
-  const int S = K / SK;
+  // K split (M == 1): column tile ct, part kp of ks, steps [s0, s0 + S)
+  const int ks = MR == 1 ? a.ksplit : 1;
+  const int ct = ks > 1 ? tile / ks : tile;
+  const int kp = tile - ct * ks;
+  const int n0 = ct * TW;
+  const int S = K / SK / ks;
+  const int s0 = kp * S;
   const int per_wave = ((S + kOneWaves - 1) / kOneWaves + NL - 1) / NL * NL;
-  const int wb = min(S, wv * per_wave);
-  const int we = min(S, wb + per_wave);
+  const int wb = s0 + min(S, wv * per_wave);
+  const int we = s0 + min(S, min(S, wv * per_wave) + per_wave);
 
   const __amdgpu_buffer_rsrc_t rq =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, kDecBufFlags);
@@ -693,6 +769,12 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       for (int j = 0; j < 4; ++j) red[wv * RSTR + (r_base + e) * RROW + part * 32 + 4 * oq + j] = tot[j][e];
   }
   __syncthreads();
+  if constexpr (MR == 1 && TW % 64 == 0) {
+    if (ks > 1) {
+      if (wv == 0) dec_split_finish<DT, TW, RSTR>(a, red, ct, kp, ks, n0, lane);
+      return;
+    }
+  }
   if (tid < MR * TW) {
     const int m = tid / TW, nl = tid - m * TW;
     const int n = n0 + nl;
@@ -806,7 +888,30 @@ struct DecPlan {
   bool cu_tiles;  // M == 1 one-workgroup-per-CU kernel (dec_kernel_one)
   int threads;
   size_t lds;
+  // K-split problems (M == 1): their pairing words, as 64-bit word offsets
+  // into the workspace's counter area
+  int64_t pair_words;
+  int64_t pair_off[W4_MAX_GROUPED];
 };
+
+// M == 1, one workgroup per CU: problems with K > 4096 are cut into ksplit
+// K parts of at most 4096 (ksplit a power of two) on 64-column tiles, i.e.
+// 256-byte pieces of the qweight rows, instead of one 32-column tile over all
+// of K (128-byte pieces).  Reading the decoder block's down_proj (2048 x 8192)
+// as two K = 4096 halves or four K = 2048 quarters took 7.5 us for the grouped
+// q/gate/up/down launch against 8.5 us with 32-column tiles (down_proj alone
+// 4.6 against 7.1 us); the 32-column tiles were the last to finish, about
+// 1.3 us after the rest.  A part must hold whole groups and whole load
+// rounds of the 64-column tiling (8 steps of 32 k): a wave's round is masked
+// as a whole past the end of its run, so a round that crossed into the next
+// part would add that part's first steps a second time.
+int one_ksplit(int64_t K, int G, int /*level*/) {
+  if (K <= 4096 || G > 4096) return 1;
+  int ks = 2;
+  while (K / ks > 4096) ks *= 2;
+  if (ks > w4::kMaxKSplit || K % ks != 0 || (K / ks) % 256 != 0 || (K / ks) % G != 0) return 1;
+  return ks;
+}
 
 // Launch table: a pure function of shapes, strides and pointer alignment.
 // Returns false (nothing launched) when a problem needs the general kernels:
@@ -820,6 +925,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int idx;
     int vec, cfg, tile_n;
     int64_t tiles, bytes_per_wg;
+    int ks;
   } items[W4_MAX_GROUPED];
   int gclass = -1;
   // every problem fits the one-workgroup-per-CU tilings (M <= 16; for M > 1
@@ -856,15 +962,19 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     }
     return tn;
   };
+  // K-split tiles (M == 1 only): 128 columns over parts of K / ksplit
+  auto tiles_at = [&](const w4a16_problem& q, int level) -> int64_t {
+    const int ks = M == 1 ? one_ksplit(q.K, G, level) : 1;
+    if (ks > 1) return (q.N + 63) / 64 * ks;
+    const int tn = one_width(q.K, level);
+    return (q.N + tn - 1) / tn;
+  };
   int level = 0;
   if (cu_tiles) {
     const int cus = device_cu_count();
     while (level < 2) {
       int64_t next = 0;
-      for (int i = 0; i < count; ++i) {
-        const int tn = one_width(problems[i].K, level + 1);
-        next += (problems[i].N + tn - 1) / tn;
-      }
+      for (int i = 0; i < count; ++i) next += tiles_at(problems[i], level + 1);
       if (next > cus) break;
       ++level;
     }
@@ -872,15 +982,16 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
-    int vec = 1, cfg = 0, tn = 16;
+    int vec = 1, cfg = 0, tn = 16, ks = 1;
     // with group 32 the per-step correction of 32 rows costs more than the
     // split-K path saves (7-launch block at M = 32: 82.0 against 76.5 us)
     if (M > 16 && q.group_size < 64) return false;
     if (cu_tiles) {
       vec = 4;
-      tn = one_width(q.K, level);
+      ks = M == 1 ? one_ksplit(q.K, G, level) : 1;
+      tn = ks > 1 ? 64 : one_width(q.K, level);
       cfg = tn == 128 ? w4::kCfgT128
-          : tn == 64  ? (q.K <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring)
+          : tn == 64  ? (q.K / ks <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring)
                       : (q.K <= 8192 ? w4::kCfgT32 : w4::kCfgT32Ring);
     } else if (q.N % 4 == 0 && qa % 16 == 0 && sa % 8 == 0 && za % 8 == 0 && q.K <= 4096) {
       vec = 4, tn = 64;
@@ -889,7 +1000,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     } else if (q.N % 2 == 0 && qa % 8 == 0 && sa % 4 == 0 && za % 4 == 0) {
       vec = 2, tn = 32;
     }
-    items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn, (int64_t)tn * q.K / 2};
+    items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn * ks, (int64_t)tn * (q.K / ks) / 2, ks};
   }
   // Longest-running workgroups first: more bytes, then longer K (narrower
   // tiles with more correction points per byte).
@@ -918,6 +1029,12 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     a.gshift = ilog2(q.group_size);
     a.vec = it.vec;
     a.cfg = it.cfg;
+    a.ksplit = it.ks;
+    a.pair = nullptr;
+    if (it.ks > 1) {
+      dp.pair_off[s] = dp.pair_words;
+      dp.pair_words += (it.tiles / it.ks) * (it.ks - 1) * it.tile_n;
+    }
     dp.g.wg_start[s] = wgs;
     if (it.tiles > (1 << 24)) return false;
     wgs += (int)it.tiles;
@@ -1008,12 +1125,38 @@ void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
 // problems need the general kernels.  sxm: activation row strides, ldy: output
 // row strides (elements; null = dense).
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
-                     int x_dtype, int64_t M, hipStream_t st) {
+                     int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
+                     hipStream_t st) {
   DecPlan dp;
   if (!dec_plan(problems, sxm, ldy, count, M, dp)) return W4_ERR_UNSUPPORTED;
+  (void)scratch;
+  (void)scratch_bytes;
+  if (dp.pair_words > 0) {
+    // K-split problems: pairing words in the workspace's counter area
+    if (dp.pair_words * 8 > W4_WORKSPACE_COUNTER_BYTES) return W4_ERR_UNSUPPORTED;
+    if (counters == nullptr)
+      return fail(W4_ERR_WORKSPACE, "w4a16 decode: a workspace of %d bytes is required",
+                  (int)W4_WORKSPACE_COUNTER_BYTES);
+    for (int s = 0; s < dp.g.count; ++s) {
+      w4::DecArgs& a = dp.g.prob[s];
+      if (a.ksplit > 1) a.pair = reinterpret_cast<unsigned long long*>(counters) + dp.pair_off[s];
+    }
+  }
   if (x_dtype == W4_DTYPE_BF16)
     dec_launch<W4_DTYPE_BF16>(dp, M, st);
   else
     dec_launch<W4_DTYPE_FP16>(dp, M, st);
   return check_launch("w4a16 decode");
+}
+
+// Workspace bytes w4_decode_launch needs for these problems: the counter area
+// (which holds the pairing words of K-split problems), or 0 when the decode
+// kernels do not take them or split nothing.  Pointers are only used for
+// their alignment, so callers without buffers may pass 256-byte-aligned
+// stand-ins.
+size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M) {
+  DecPlan dp;
+  if (!dec_plan(problems, sxm, nullptr, count, M, dp)) return 0;
+  if (dp.pair_words == 0 || dp.pair_words * 8 > W4_WORKSPACE_COUNTER_BYTES) return 0;
+  return W4_WORKSPACE_COUNTER_BYTES;
 }

@@ -40,7 +40,9 @@ static constexpr int64_t kDecodeM = 16;
 static constexpr int64_t kDecode32M = 32;
 
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
-                     int x_dtype, int64_t M, hipStream_t st);
+                     int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
+                     hipStream_t st);
+size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
 
 // Every workspace starts with a W4_WORKSPACE_COUNTER_BYTES area of per-tile
 // arrival counters (zero before first use, left zero by every call), then
@@ -111,7 +113,7 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
                           counters, scratch, scratch_bytes, st);
   if (M <= kDecode32M && stride_xk == 1) {
     const w4a16_problem q{x, qweight, scales, zeros, y, N, K, (int32_t)G, 0};
-    const int rc = w4_decode_launch(&q, &stride_xm, &ldy, 1, x_dtype, M, st);
+    const int rc = w4_decode_launch(&q, &stride_xm, &ldy, 1, x_dtype, M, counters, scratch, scratch_bytes, st);
     if (rc != W4_ERR_UNSUPPORTED) return rc;
   }
   if (M <= kSmallM) {
@@ -153,8 +155,14 @@ extern "C" size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, i
     }
     return most;
   }
-  const int64_t scratch = w4_gemv_grouped_scratch_bytes(problems, count, M);
-  return scratch > 0 ? W4_WORKSPACE_COUNTER_BYTES + (size_t)scratch : 0;
+  // the decode kernel's K split (counter area only), or the grouped gemv
+  // kernel's partials (groups below 32): room for either
+  int64_t sxm[W4_MAX_GROUPED];
+  for (int i = 0; i < count; ++i) sxm[i] = problems[i].K;
+  const int64_t grp = w4_gemv_grouped_scratch_bytes(problems, count, M);
+  const size_t dec = w4_decode_workspace_bytes(problems, sxm, count, M);  // counter area only
+  if (grp > 0) return W4_WORKSPACE_COUNTER_BYTES + (size_t)grp;
+  return dec;
 }
 
 extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
@@ -173,7 +181,7 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
     if (M <= kDecode32M) {
       int64_t sxm[W4_MAX_GROUPED];
       for (int i = 0; i < count; ++i) sxm[i] = problems[i].K;
-      const int drc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, M, st);
+      const int drc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, M, nullptr, nullptr, 0, st);
       if (drc != W4_ERR_UNSUPPORTED) return drc;
     }
     const int grc = w4_prefill_grouped_launch(problems, count, x_dtype, M, st);

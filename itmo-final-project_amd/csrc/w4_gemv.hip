@@ -485,15 +485,24 @@ bool plan_grouped(const w4a16_problem* problems, int count, int64_t M, GroupedPl
 // Scratch bytes (past the workspace's counter area) of the single-problem
 // paths.  M == 1 runs as a one-problem grouped launch (partials finished
 // in-kernel); 2 <= M <= 16 writes fp32 partials for the reduce kernel.
+size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
+
 size_t w4_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int G) {
   if (M == 1) {
+    // the decode kernel's K split (aligned operands; counter area only) or the
+    // grouped gemv kernel's split partials (groups below 32): room for either
+    static char aligned_stand_in[256] __attribute__((aligned(256)));
+    w4a16_problem q{aligned_stand_in, reinterpret_cast<const int32_t*>(aligned_stand_in),
+                    reinterpret_cast<const uint16_t*>(aligned_stand_in),
+                    reinterpret_cast<const uint16_t*>(aligned_stand_in), aligned_stand_in, N, K, G, 0};
+    const int64_t sx = K;
+    // the decode kernel's split needs the counter area only: one byte of
+    // scratch makes the caller's size query non-zero
+    const size_t dec = w4_decode_workspace_bytes(&q, &sx, 1, 1) > 0 ? 1 : 0;
     GroupedPlan gp;
-    w4a16_problem q{};
-    q.N = N;
-    q.K = K;
-    q.group_size = G;
-    if (!plan_grouped(&q, 1, 1, gp)) return 0;
-    return gp.float_count * sizeof(float);
+    if (!plan_grouped(&q, 1, 1, gp)) return dec;
+    const size_t grp = gp.float_count * sizeof(float);
+    return grp > dec ? grp : dec;
   }
   const size_t a = plan_gemv(M, N, K, (N % 4) == 0).ws;
   const size_t b = plan_gemv(M, N, K, false).ws;
@@ -511,7 +520,9 @@ int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K
                      void* ws, size_t ws_bytes, hipStream_t st);
 
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
-                     int x_dtype, int64_t M, hipStream_t st);
+                     int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
+                     hipStream_t st);
+size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
 
 int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
                    const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, void* y, int64_t ldy,
@@ -526,7 +537,7 @@ int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, 
   {
     // group size >= 32: factored single-launch decode kernel (w4_decode.hip)
     const w4a16_problem q{x, qw, sc, ze, y, N, K, G, 0};
-    const int rc = w4_decode_launch(&q, &sxm, &ldy, 1, x_dtype, M, st);
+    const int rc = w4_decode_launch(&q, &sxm, &ldy, 1, x_dtype, M, counters, ws, ws_bytes, st);
     if (rc != W4_ERR_UNSUPPORTED) return rc;
   }
   // M == 1: the grouped kernel with its in-kernel split fixup.  Without a
@@ -574,7 +585,7 @@ int w4_gemv_grouped_launch(const w4a16_problem* problems, int count, int x_dtype
   if (count >= 1 && count <= W4_MAX_GROUPED) {
     int64_t sxm[W4_MAX_GROUPED];
     for (int i = 0; i < count; ++i) sxm[i] = problems[i].K;
-    const int rc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, M, st);
+    const int rc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, M, counters, scratch, scratch_bytes, st);
     if (rc != W4_ERR_UNSUPPORTED) return rc;
   }
   GroupedPlan gp;

@@ -209,6 +209,17 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
     return [y.reshape(*x.shape[:-1], y.shape[-1]) for x, y in zip(xs, outs)]
 
 
+def grouped_workspace_bytes(xs: Sequence[torch.Tensor], weights: Sequence[tuple]) -> int:
+    """Workspace bytes ``w4a16_matmul_grouped(xs, weights)`` uses (0 if none)."""
+    M = xs[0].reshape(-1, xs[0].shape[-1]).shape[0]
+    probs = (_lib.Problem * len(xs))()
+    for i, (x, (qw, s, z)) in enumerate(zip(xs, weights)):
+        K = x.shape[-1]
+        probs[i] = _lib.Problem(x.data_ptr(), qw.data_ptr(), s.data_ptr(), z.data_ptr(), x.data_ptr(), qw.shape[1],
+                                K, K // s.shape[0], 0)
+    return _lib.load().w4a16_grouped_workspace_bytes(probs, len(xs), M)
+
+
 def w16a16_matmul(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """x[..., K] @ w[N, K]^T with full-precision weights (the reference's W16 baseline,
     int4_triton/gemm.py:312-317).

@@ -338,3 +338,28 @@ def test_strided_rows_workspace_on_new_stream(M, N, K):
     torch.cuda.synchronize()
     _check(out, x, qw, s, z, ref_unrounded=False)
     assert torch.equal(again.view(torch.int16), out.view(torch.int16))
+
+
+# M = 1 with K > 4096: the decode kernel splits K into two or four parts on
+# 64-column tiles whose partial sums meet pairwise through 64-bit
+# compare-and-swap words (one or two tree levels); every repeat, with the
+# outputs poisoned in between, must give the same bits, lone and grouped
+@pytest.mark.parametrize("N,K,G", [(2048, 8192, 128), (1024, 16384, 64), (200, 6144, 32), (72, 12288, 128)])
+def test_decode_ksplit_pairs_repeat(N, K, G):
+    print(f"[ksplit] N={N} K={K} G={G}", flush=True)
+    qw, s, z = _weights(N, K, G, seed=N + K + G)
+    x = randn((1, K), seed=K + 1).to(DEV)
+    first = int4_hip.w4a16_matmul(x, qw, s, z)
+    _check(first, x, qw, s, z, ref_unrounded=False, exact_w=True)
+    other = [_weights(2048, 2048, G, seed=9), randn((1, 2048), seed=10).to(DEV)]
+    grouped_first = None
+    for _ in range(4):
+        y = torch.full((1, N), float("nan"), dtype=torch.bfloat16, device=DEV)
+        again = int4_hip.w4a16_matmul(x, qw, s, z)
+        assert torch.equal(again.view(torch.int16), first.view(torch.int16))
+        yo = torch.full((1, 2048), float("nan"), dtype=torch.bfloat16, device=DEV)
+        int4_hip.w4a16_matmul_grouped([x, other[1]], [(qw, s, z), other[0]], out=[y, yo])
+        if grouped_first is None:
+            _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+            grouped_first = y.clone()
+        assert torch.equal(y.view(torch.int16), grouped_first.view(torch.int16))
