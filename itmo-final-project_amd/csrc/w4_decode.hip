@@ -905,11 +905,20 @@ struct DecPlan {
 // rounds of the 64-column tiling (8 steps of 32 k): a wave's round is masked
 // as a whole past the end of its run, so a round that crossed into the next
 // part would add that part's first steps a second time.
-int one_ksplit(int64_t K, int G, int /*level*/) {
+// Each narrowing level (a launch with few workgroups: a lone linear) halves
+// the parts again while they stay whole rounds and groups, so a lone down_proj
+// runs 256 workgroups of 32 KB instead of 64 of 128 KB.
+// The pairing words ((ks - 1) per column) live in the workspace's counter area.
+int one_ksplit(int64_t K, int G, int level, int64_t N) {
   if (K <= 4096 || G > 4096) return 1;
   int ks = 2;
   while (K / ks > 4096) ks *= 2;
-  if (ks > w4::kMaxKSplit || K % ks != 0 || (K / ks) % 256 != 0 || (K / ks) % G != 0) return 1;
+  auto ok = [&](int k) {
+    return k <= w4::kMaxKSplit && K % k == 0 && (K / k) % 256 == 0 && (K / k) % G == 0 &&
+           (N + 63) / 64 * 64 * (int64_t)(k - 1) * 8 <= W4_WORKSPACE_COUNTER_BYTES;
+  };
+  if (!ok(ks)) return 1;
+  for (int l = 0; l < level && ok(2 * ks); ++l) ks *= 2;
   return ks;
 }
 
@@ -964,7 +973,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   };
   // K-split tiles (M == 1 only): 128 columns over parts of K / ksplit
   auto tiles_at = [&](const w4a16_problem& q, int level) -> int64_t {
-    const int ks = M == 1 ? one_ksplit(q.K, G, level) : 1;
+    const int ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : 1;
     if (ks > 1) return (q.N + 63) / 64 * ks;
     const int tn = one_width(q.K, level);
     return (q.N + tn - 1) / tn;
@@ -988,7 +997,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     if (M > 16 && q.group_size < 64) return false;
     if (cu_tiles) {
       vec = 4;
-      ks = M == 1 ? one_ksplit(q.K, G, level) : 1;
+      ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : 1;
       tn = ks > 1 ? 64 : one_width(q.K, level);
       cfg = tn == 128 ? w4::kCfgT128
           : tn == 64  ? (q.K / ks <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring)
