@@ -8,7 +8,8 @@ down 2048x8192; N x K), G=128, bf16 activations, as ONE grouped launch
 (``w4a16_matmul_grouped``).  Step i uses weight set i % 16: 16 distinct
 seeded sets (16 x 32.3 MB > the 256 MB Infinity Cache) so weights stream from
 HBM.  Inputs are resident in HBM before the timed region.  Exactly --warmup
-untimed steps run, then exactly --steps timed steps as one graph replay
+untimed steps run, then exactly --steps timed steps, each one call of the
+library's C-ABI grouped entry point issued back to back from a C loop,
 bracketed by host synchronisation and HIP events on the launch stream.
 
 Printed (last line, JSON): ``value`` = algorithmic HBM bytes of the block
@@ -71,30 +72,6 @@ def graph_of(fn, stream, eager_warmup: bool = True):
             fn()
     torch.cuda.synchronize()
     return g
-
-
-def upload_graph(g, stream) -> bool:
-    """hipGraphUpload of a captured graph's executable on ``stream``, so that its
-    first replay does not pay the one-time upload (about 10 us measured on a
-    fresh 20-launch graph).  Runs no kernel.  False if the handle or the call
-    is not available."""
-    import ctypes
-
-    import torch
-
-    try:
-        exe = g.raw_cuda_graph_exec()
-        exe = int(exe) if not isinstance(exe, int) else exe
-        hip = ctypes.CDLL("libamdhip64.so.7")  # the HIP runtime torch already loaded
-        fn = hip.hipGraphUpload
-        fn.restype = ctypes.c_int
-        fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
-        rc = fn(ctypes.c_void_p(exe), ctypes.c_void_p(stream.cuda_stream))
-        torch.cuda.synchronize()
-        return rc == 0
-    except Exception as e:  # older torch / other runtime: the first replay includes the upload
-        log(f"graph upload unavailable ({e!r})")
-        return False
 
 
 def time_graph_once(g, stream) -> float:
@@ -479,36 +456,69 @@ def main() -> int:
     ms_per_step = kern_ms = value = achieved = steady_ms = None
     kern_ms_src = None
     if "decode" in only:
-        # exactly `warm` untimed steps (eager, on the launch stream: they also
-        # create the stream's persistent split-K workspace), then exactly
-        # `steps` timed ones as one graph replay: step i is one grouped launch
-        # over weight set i % nsets.  Capturing runs nothing.
-        def run(n):
-            return lambda: [grouped(i % nsets)() for i in range(n)]
+        # Exactly `warm` untimed steps, then exactly `steps` timed ones, each
+        # step one call of the library's grouped entry point (the one
+        # w4a16_matmul_grouped makes) on weight set i % nsets, issued back to
+        # back from a C loop (csrc/bench/launch_loop.cpp) so that the GPU, not
+        # the interpreter, sets the pace; HIP events on the launch stream
+        # bracket the timed calls, host synchronisation on both sides.
+        import ctypes
 
-        with torch.cuda.stream(stream):
-            run(warm)()
-            if warm == 0:  # no warm-up step: reserve the workspace without running one
-                nb = int4_hip.gemm.grouped_workspace_bytes(xs1[0], packed[0])
-                if nb:
-                    int4_hip.gemm._stream_workspace(dev, stream.cuda_stream, nb)
-        torch.cuda.synchronize()
-        g_main = graph_of(run(steps), stream, eager_warmup=False)
-        uploaded = upload_graph(g_main, stream)
-        ms_run = time_graph_once(g_main, stream)
+        lib = int4_hip._lib.load()
+        blib_path = ROOT / "itmo-final-project_amd" / "int4_hip" / "libw4_bench.so"
+        nprob = len(LINEARS)
+        probs = (int4_hip._lib.Problem * (nprob * nsets))()
+        for i in range(nsets):
+            for j, (x, (qw, sc, ze), y) in enumerate(zip(xs1[i], packed[i], ys1[i])):
+                K = x.shape[1]
+                probs[i * nprob + j] = int4_hip._lib.Problem(x.data_ptr(), qw.data_ptr(), sc.data_ptr(), ze.data_ptr(),
+                                                             y.data_ptr(), qw.shape[1], K, K // sc.shape[0], 0)
+        ws_need = lib.w4a16_grouped_workspace_bytes(probs, nprob, 1)
+        ws = int4_hip.gemm._stream_workspace(dev, stream.cuda_stream, ws_need) if ws_need else None
+        ws_ptr, ws_len = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+        fn_ptr = ctypes.cast(lib.w4a16_gemm_grouped, ctypes.c_void_p).value
+        blib = ctypes.CDLL(str(blib_path)) if blib_path.exists() else None
+        if blib is not None:
+            loop = blib.w4bench_grouped_steps
+            loop.restype = ctypes.c_int
+            loop.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
+                             ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t,
+                             ctypes.c_void_p]
+
+            def c_steps(n):
+                rc = loop(fn_ptr, ctypes.cast(probs, ctypes.c_void_p), ctypes.sizeof(int4_hip._lib.Problem) * nprob,
+                          nprob, nsets, n, int4_hip._lib.DTYPE_BF16, 1, ws_ptr, ws_len, stream.cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"w4a16_gemm_grouped failed in the step loop ({rc})")
+
+            c_steps(warm)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            c_steps(steps)
+            e1.record(stream)
+            torch.cuda.synchronize()
+            ms_run = e0.elapsed_time(e1)
+            kern_ms_src = "hip-events-on-launch-stream-over-the-timed-steps (C loop of C-ABI calls)"
+        else:  # no bench helper: the timed steps as one graph replay
+            with torch.cuda.stream(stream):
+                for i in range(warm):
+                    grouped(i % nsets)()
+            torch.cuda.synchronize()
+            g_steps = graph_of(lambda: [grouped(i % nsets)() for i in range(steps)], stream, eager_warmup=False)
+            ms_run = time_graph_once(g_steps, stream)
+            del g_steps
+            kern_ms_src = "hip-events-on-launch-stream-over-the-timed-steps (one graph replay)"
         ms_per_step = ms_run / steps
         value = bytes1 / (ms_per_step * 1e-3) / 1e9
         # one kernel per step: the roofline kernel's average duration is the
-        # timed region over its launches (HIP events on the launch stream)
-        kern_ms, kern_ms_src = ms_per_step, ("hip-events-on-launch-stream-over-the-timed-steps"
-                                             + (", graph uploaded before timing" if uploaded else ""))
+        # timed region over its launches
+        kern_ms = ms_per_step
         achieved = bytes1 / (kern_ms * 1e-3) / 1e9
-        # steady state beside it: the same graph replayed back to back (the
-        # timed single replay above also carries the first replay of a fresh
-        # graph, about 0.45 us per launch, and the idle-to-busy start, about
-        # 7 us, spread over its steps)
+        # steady state beside it: a graph of the 16 sets replayed back to back
+        g_main = graph_of(lambda: [grouped(i)() for i in range(nsets)], stream)
         time_graph(g_main, 2, stream)
-        steady_ms = time_graph(g_main, 10, stream) / steps
+        steady_ms = time_graph(g_main, 10, stream) / nsets
         del g_main
 
     # ------------------------------------------------- M=1 per-linear launches (reference-comparable)

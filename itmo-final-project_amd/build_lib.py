@@ -74,7 +74,7 @@ def build(jobs: int | None = None, verbose: bool = True) -> Path:
     if r.returncode != 0:
         raise RuntimeError(f"link failed\n{' '.join(cmd)}\n{r.stderr}")
     os.replace(tmp, LIB)
-    bench_srcs = sorted(BENCH_SRC.glob("*.hip"))
+    bench_srcs = sorted(list(BENCH_SRC.glob("*.hip")) + list(BENCH_SRC.glob("*.cpp")))
     if bench_srcs:
         bobjs = [_compile(s) for s in bench_srcs]
         btmp = BENCH_LIB.with_suffix(".so.tmp")
