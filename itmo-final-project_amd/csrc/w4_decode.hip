@@ -927,7 +927,7 @@ int one_ksplit(int64_t K, int G, int level, int64_t N) {
 // group size < 32, mixed group-size classes, misaligned or non-dense
 // activations, or offsets past 2 GiB.
 bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int64_t M,
-              DecPlan& dp) {
+              DecPlan& dp, const int64_t* mrows = nullptr) {
   dp = DecPlan{};
   if (count < 1 || count > W4_MAX_GROUPED || M < 1 || M > 32) return false;
   struct Item {
@@ -947,7 +947,9 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     if (gclass >= 0 && ilog2(q.group_size) != ilog2(problems[0].group_size)) return false;
     gclass = 0;
     if (((uintptr_t)q.x % 16) != 0) return false;
-    if (M > 1 && ((sxm[i] % 8) != 0 || sxm[i] < q.K || ((M - 1) * sxm[i] + q.K) * 2 >= (1LL << 31))) return false;
+    const int64_t Mi = mrows != nullptr ? mrows[i] : M;  // rows of this problem (<= M)
+    if (Mi < 1 || Mi > M) return false;
+    if (M > 1 && ((sxm[i] % 8) != 0 || sxm[i] < q.K || ((Mi - 1) * sxm[i] + q.K) * 2 >= (1LL << 31))) return false;
     if (ldy != nullptr && ldy[i] < q.N) return false;
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
@@ -1031,10 +1033,11 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     a.ldy = ldy != nullptr ? ldy[it.idx] : q.N;
     a.qw_bytes = (uint32_t)((q.K / 8) * q.N * 4);
     a.sz_bytes = (uint32_t)((q.K / q.group_size) * q.N * 2);
-    a.x_bytes = (uint32_t)(((M - 1) * a.sxm + q.K) * 2);
+    const int64_t Mi = mrows != nullptr ? mrows[it.idx] : M;
+    a.x_bytes = (uint32_t)(((Mi - 1) * a.sxm + q.K) * 2);
     a.N = (int)q.N;
     a.K = (int)q.K;
-    a.M = (int)M;
+    a.M = (int)Mi;
     a.gshift = ilog2(q.group_size);
     a.vec = it.vec;
     a.cfg = it.cfg;
@@ -1132,12 +1135,13 @@ void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
 // Factored decode launch (see the top of this file).  Returns
 // W4_ERR_UNSUPPORTED, with nothing launched and no error message, when the
 // problems need the general kernels.  sxm: activation row strides, ldy: output
-// row strides (elements; null = dense).
+// row strides (elements; null = dense); mrows: rows of each problem (null: M
+// for all; each <= M, the launch's row count, which picks the kernel).
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
-                     hipStream_t st) {
+                     hipStream_t st, const int64_t* mrows) {
   DecPlan dp;
-  if (!dec_plan(problems, sxm, ldy, count, M, dp)) return W4_ERR_UNSUPPORTED;
+  if (!dec_plan(problems, sxm, ldy, count, M, dp, mrows)) return W4_ERR_UNSUPPORTED;
   (void)scratch;
   (void)scratch_bytes;
   if (dp.pair_words > 0) {

@@ -521,7 +521,7 @@ int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K
 
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
-                     hipStream_t st);
+                     hipStream_t st, const int64_t* mrows = nullptr);
 size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
 
 int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,

@@ -254,18 +254,19 @@ def test_grouped_shared_activation(M, K, Ns, G):
     print(f"[grouped-prefill] M={M} K={K} Ns={Ns} G={G}", flush=True)
     ws = [_weights(N, K, G, seed=400 + i) for i, N in enumerate(Ns)]
     x = randn((M, K), seed=410 + M).to(DEV)
-    # M <= 32 with K <= 4096 and G >= 64: one decode launch (exact W_hat)
-    ew = all(_decode(M, G, N, K) for N in Ns)
+    # M <= 64: decode launches (exact W_hat) or, where the library's plan
+    # prefers it, one shared-activation prefill launch (W_hat rounded)
+    ew = "either" if M <= 64 else False
     outs = int4_hip.w4a16_matmul_grouped([x] * len(Ns), ws)
     for (qw, s, z), y in zip(ws, outs):
-        _check(y, x, qw, s, z, ref_unrounded=not ew, exact_w=ew)
+        _check(y, x, qw, s, z, ref_unrounded=True, exact_w=ew)
     again = int4_hip.w4a16_matmul_grouped([x] * len(Ns), ws)
     for a, b in zip(outs, again):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
     xs = [randn((M, K), seed=420 + i).to(DEV) for i in range(len(Ns))]
     mixed = int4_hip.w4a16_matmul_grouped(xs, ws)
     for xi, (qw, s, z), y in zip(xs, ws, mixed):
-        _check(y, xi, qw, s, z, ref_unrounded=not ew, exact_w=ew)
+        _check(y, xi, qw, s, z, ref_unrounded=True, exact_w=ew)
 
 
 def _replays_match(g, out, eager, reps=3):

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import int4_hip
-from _checks import _check
+from _checks import _check, _decode
 from _synth import randn
 from int4_hip.llama import GraphDecoder, LlamaConfig, LlamaForCausalLM, argmax_last, run_eval
 
@@ -132,7 +132,7 @@ def test_int4linear_from_reference_written_buffers():
         print(f"[golden buffers] M={M}", flush=True)
         x = randn((M, K), seed=40 + M).to(DEV)
         _check(layer(x), x, layer.qweight, layer.scales, layer.zeros, ref_unrounded=False,
-               exact_w=M <= 16)
+               exact_w=_decode(M, K // s.shape[0]))
 
 
 # ------------------------------------------------- full-size Llama-3.2-1B
