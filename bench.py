@@ -585,7 +585,7 @@ def main() -> int:
                 if g == G and M == 16:
                     ms16 = msm
                 del gm
-                if M <= 16:
+                if M <= 64:
                     # all seven products in one launch (as the M=1 headline figure)
                     gg = graph_of(lambda: [int4_hip.w4a16_matmul_grouped(xsm, packs[i]) for i in range(nsets)],
                                   stream)

@@ -63,7 +63,31 @@ struct DecArgs {
   // (zero on entry and left zero), see dec_split_finish.
   int ksplit;
   unsigned long long* pair;
+  // 16-row launches: M may exceed 16; the problem is then cut into `slices`
+  // row slices of 16, workgroup tile t covering column tile t % col_tiles of
+  // rows [16 s, 16 s + 16), s = t / col_tiles (see dec_row_slice)
+  int slices;
+  int col_tiles;
 };
+
+// The column tile and row slice of tile `tile` of a 16-row problem: a copy of
+// the problem's arguments with x, y, M and the activation range narrowed to the
+// slice.  Slice-major order keeps the slices of one column tile on one XCD
+// when col_tiles is a multiple of 8 (workgroups go to the XCDs round-robin),
+// so their reads of the same weights meet in that XCD's L2.
+__device__ __forceinline__ DecArgs dec_row_slice(const DecArgs& g, int& tile) {
+  DecArgs a = g;
+  if (g.slices > 1) {
+    const int s = tile / g.col_tiles;
+    tile -= s * g.col_tiles;
+    const int r0 = 16 * s;
+    a.x = g.x + (int64_t)r0 * g.sxm;
+    a.y = g.y + (int64_t)r0 * g.ldy;
+    a.M = min(16, g.M - r0);
+    a.x_bytes = (uint32_t)(((int64_t)(a.M - 1) * g.sxm + g.K) * 2);
+  }
+  return a;
+}
 
 // M == 1 tilings (dec_kernel_one)
 constexpr int kCfgT128 = 0;     // 128 columns, one round of 8 loads per wave (K <= 2048)
@@ -508,6 +532,7 @@ constexpr int one_lds(int mr) {
 // them in part order and writes y, then leaves the counter at zero.  Every
 // output bit is a function of the inputs only.
 constexpr int kMaxKSplit = 8;  // K parts of one M == 1 column tile
+constexpr int kMaxRowSlices = 4;  // 16-row slices of one problem (M <= 64)
 
 // K-split tile (M == 1): wave 0 sums the per-wave partials of each of the
 // tile's columns (one or two per lane, the fixed wave order of the unsplit
@@ -840,8 +865,10 @@ __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) 
       default: dec_tile_one<DT, 32, G32, 8, 1, MR>(a, tile, lds); break;
     }
   } else {
-    // sixteen rows: the 64-column tiling only
-    dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds);
+    // sixteen rows: the 64-column tiling only, problems of more rows in slices
+    int st = tile;
+    const DecArgs as = dec_row_slice(a, st);
+    dec_tile_one<DT, 64, G64, 8, 1, MR>(as, st, lds);
   }
 }
 
@@ -859,9 +886,18 @@ __global__ __launch_bounds__(kDecThreads) void dec_kernel(DecGroupedArgs g) {
   // !ONE: [activation areas: 8 waves x MX x 4C x 16 B], reused for the reduction
   uint32_t* xl = reinterpret_cast<uint32_t*>(dec_smem);
   float* red = dec_smem + kDecWaves * 64 * 4;
-  if constexpr (MX == 32)  // the host gives 32-row launches 64-column tiles only
+  if constexpr (MX == 32) {  // the host gives 32-row launches 64-column tiles only
     dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4), MX>(a, tile, red, xl);
-  else if (a.vec == 4)
+  } else if constexpr (MX == 16) {  // problems of more rows in 16-row slices
+    int st = tile;
+    const DecArgs as = dec_row_slice(a, st);
+    if (as.vec == 4)
+      dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4), MX>(as, st, red, xl);
+    else if (as.vec == 2)
+      dec_tile<DT, 2, ONE, GS, MX>(as, st, red, xl);
+    else
+      dec_tile<DT, 1, ONE, GS, MX>(as, st, red, xl);
+  } else if (a.vec == 4)
     dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4), MX>(a, tile, red, xl);
   else if (a.vec == 2)
     dec_tile<DT, 2, ONE, GS, MX>(a, tile, red, xl);
@@ -934,7 +970,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int idx;
     int vec, cfg, tile_n;
     int64_t tiles, bytes_per_wg;
-    int ks;
+    int ks, slices;
   } items[W4_MAX_GROUPED];
   int gclass = -1;
   // every problem fits the one-workgroup-per-CU tilings (M <= 16; for M > 1
@@ -947,8 +983,10 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     if (gclass >= 0 && ilog2(q.group_size) != ilog2(problems[0].group_size)) return false;
     gclass = 0;
     if (((uintptr_t)q.x % 16) != 0) return false;
-    const int64_t Mi = mrows != nullptr ? mrows[i] : M;  // rows of this problem (<= M)
-    if (Mi < 1 || Mi > M) return false;
+    // rows of this problem: at most M, or with M == 16 up to kMaxRowSlices
+    // slices of 16 rows
+    const int64_t Mi = mrows != nullptr ? mrows[i] : M;
+    if (Mi < 1 || (Mi > M && (M != 16 || Mi > 16 * w4::kMaxRowSlices))) return false;
     if (M > 1 && ((sxm[i] % 8) != 0 || sxm[i] < q.K || ((Mi - 1) * sxm[i] + q.K) * 2 >= (1LL << 31))) return false;
     if (ldy != nullptr && ldy[i] < q.N) return false;
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
@@ -1011,7 +1049,9 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     } else if (q.N % 2 == 0 && qa % 8 == 0 && sa % 4 == 0 && za % 4 == 0) {
       vec = 2, tn = 32;
     }
-    items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn * ks, (int64_t)tn * (q.K / ks) / 2, ks};
+    const int64_t Mi = mrows != nullptr ? mrows[i] : M;
+    const int slices = (int)((Mi + M - 1) / M);  // > 1 only for 16-row launches
+    items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn * ks * slices, (int64_t)tn * (q.K / ks) / 2, ks, slices};
   }
   // Longest-running workgroups first: more bytes, then longer K (narrower
   // tiles with more correction points per byte).
@@ -1043,6 +1083,8 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     a.cfg = it.cfg;
     a.ksplit = it.ks;
     a.pair = nullptr;
+    a.slices = it.slices;
+    a.col_tiles = (int)(it.tiles / it.slices);
     if (it.ks > 1) {
       dp.pair_off[s] = dp.pair_words;
       dp.pair_words += (it.tiles / it.ks) * (it.ks - 1) * it.tile_n;

@@ -34,14 +34,9 @@ int w4_prefill_grouped_launch(const w4a16_problem* problems, int count, int x_dt
 static constexpr int64_t kSmallM = 64;
 // Decode-shaped products (activations staged in LDS) up to this M.
 static constexpr int64_t kDecodeM = 16;
-// Up to this M, products whose every operand fits the decode kernel's
-// 64-column tiles (K <= 4096, group >= 64, aligned, dense activation rows) take
-// it too (two 16-row MFMA blocks, no split-K partials); others the split-K path.
-static constexpr int64_t kDecode32M = 32;
-// Up to this M, dense rows run as slices of kDecodeM rows in one grouped
-// decode launch (W4_MAX_GROUPED slices at most).
+// Up to this M, dense rows run as row slices of kDecodeM in one decode
+// launch (four slices at most).
 static constexpr int64_t kSliceM = 64;
-static_assert(kSliceM <= kDecodeM * W4_MAX_GROUPED, "row slices of one launch");
 
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
@@ -116,26 +111,12 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
     return w4_gemv_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
                           counters, scratch, scratch_bytes, st);
   if (M <= kSliceM && stride_xk == 1) {
-    // 17 <= M <= 64: the rows as slices of at most kDecodeM, each a problem of
-    // one grouped decode launch (the weights are read once per slice, the
-    // repeats mostly from the caches): no split-K partials, no reduce launch
-    const int ns = (int)((M + kDecodeM - 1) / kDecodeM);
-    w4a16_problem qs[W4_MAX_GROUPED];
-    int64_t sx[W4_MAX_GROUPED], ly[W4_MAX_GROUPED], mr[W4_MAX_GROUPED];
-    for (int i = 0; i < ns; ++i) {
-      const int64_t r0 = (int64_t)i * kDecodeM;
-      qs[i] = w4a16_problem{static_cast<const uint16_t*>(x) + r0 * stride_xm, qweight, scales, zeros,
-                            static_cast<uint16_t*>(y) + r0 * ldy, N, K, (int32_t)G, 0};
-      sx[i] = stride_xm;
-      ly[i] = ldy;
-      mr[i] = M - r0 < kDecodeM ? M - r0 : kDecodeM;
-    }
-    const int rc = w4_decode_launch(qs, sx, ly, ns, x_dtype, kDecodeM, counters, scratch, scratch_bytes, st, mr);
-    if (rc != W4_ERR_UNSUPPORTED) return rc;
-  }
-  if (M <= kDecode32M && stride_xk == 1) {
+    // 17 <= M <= 64: the rows as slices of kDecodeM in one decode launch (the
+    // weights are read once per slice, the repeats mostly from L2): no split-K
+    // partials, no reduce launch
     const w4a16_problem q{x, qweight, scales, zeros, y, N, K, (int32_t)G, 0};
-    const int rc = w4_decode_launch(&q, &stride_xm, &ldy, 1, x_dtype, M, counters, scratch, scratch_bytes, st);
+    const int rc = w4_decode_launch(&q, &stride_xm, &ldy, 1, x_dtype, kDecodeM, counters, scratch, scratch_bytes,
+                                    st, &M);
     if (rc != W4_ERR_UNSUPPORTED) return rc;
   }
   if (M <= kSmallM) {
@@ -200,10 +181,11 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
     // else one w4a16_gemm per problem, in order, on the stream (x rows of K
     // elements)
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (M <= kDecode32M) {
-      int64_t sxm[W4_MAX_GROUPED];
-      for (int i = 0; i < count; ++i) sxm[i] = problems[i].K;
-      const int drc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, M, nullptr, nullptr, 0, st);
+    if (M <= kSliceM) {
+      int64_t sxm[W4_MAX_GROUPED], mr[W4_MAX_GROUPED];
+      for (int i = 0; i < count; ++i) sxm[i] = problems[i].K, mr[i] = M;
+      const int drc =
+          w4_decode_launch(problems, sxm, nullptr, count, x_dtype, kDecodeM, nullptr, nullptr, 0, st, mr);
       if (drc != W4_ERR_UNSUPPORTED) return drc;
     }
     const int grc = w4_prefill_grouped_launch(problems, count, x_dtype, M, st);
