@@ -82,6 +82,7 @@ def time_graph_once(g, stream) -> float:
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    host_spin(2.0)
     with torch.cuda.stream(stream):
         e0.record(stream)
         g.replay()
@@ -97,6 +98,7 @@ def time_graph(g, reps: int, stream) -> float:
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
+    host_spin(2.0)
     with torch.cuda.stream(stream):
         e0.record(stream)
         for _ in range(reps):
@@ -303,6 +305,17 @@ PROFILE = ROOT / "profiles" / "dec_kernel_one_decode_block_m1.md"
 ROOFLINE_KERNEL = "dec_kernel_one<0, 2, 1>"
 
 
+def host_spin(ms: float) -> None:
+    """Keep this host core busy for `ms` milliseconds, outside any timed
+    region.  After a synchronisation that waited a while the core idles at a
+    low clock, and the first ~20 library calls that follow take 6-8 us of
+    host time each instead of about 3 (measured on the MI355X box), so a short
+    run of steps would measure the host's wake-up instead of the GPU."""
+    end = time.perf_counter() + ms * 1e-3
+    while time.perf_counter() < end:
+        pass
+
+
 def summarize_prof(d: Path, kernel: str = ROOFLINE_KERNEL) -> str:
     """Markdown lines from a rocprofv3 run directory laid out as
     ``trace/`` (--kernel-trace --stats), ``fetch/`` (--pmc FETCH_SIZE),
@@ -494,6 +507,7 @@ def main() -> int:
             c_steps(warm)
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            host_spin(2.0)
             e0.record(stream)
             c_steps(steps)
             e1.record(stream)

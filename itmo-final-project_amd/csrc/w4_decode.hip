@@ -1,5 +1,6 @@
-// Decode-shaped W4A16 products (1 <= M <= 16, group size >= 32) for gfx950:
-// one launch, no split-K, the dequantization factored out of the K loop.
+// Decode-shaped W4A16 products (1 <= M <= 16, group size >= 32; up to 64
+// rows as 16-row slices of one launch) for gfx950: one launch, no fp32
+// partials in memory, the dequantization factored out of the K loop.
 //
 // Arithmetic.  For one output column n and one quantization group g,
 //   sum_k x_k (q_k - z) s = s * ( sum_k x_k (OFF + QS q_k) - OFF xs - QS z xs ) / QS
@@ -260,11 +261,10 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   constexpr int D = DecChunk<VEC>::D;
   constexpr int NP = C / GS;  // correction points per chunk
   constexpr int R = ONE ? 1 : 4;
-  constexpr int RB = MX > 16 ? 2 : 1;    // 16-row MFMA blocks (MX = 32: rows 0..15, 16..31)
   constexpr int C4 = 4 * C;              // 16-byte activation slices per row and chunk
   constexpr int XL = ONE ? 1 : MX * C / 16;  // activation loads per chunk and lane
   static_assert(GS >= 1 && GS <= C && (C % GS) == 0, "correction interval");
-  static_assert(ONE || (XL >= 1 && (MX <= C4 || (MX == 32 && VEC == 4)) && MX <= 32), "activation staging");
+  static_assert(ONE || (XL >= 1 && MX <= C4 && MX <= 16), "activation staging");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -305,15 +305,10 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
       x_off[j] = m < M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)sl * 16u : kDecOOB;
     }
   }
-  // read slot of step 0 for block b (row 16 b + c, rows past M repeat row
-  // M - 1); step st adds 4 st inside the XOR.  Slice s of row m sits at slot
-  // C4 m + (s ^ (m % C4)).
-  int x_rd[RB];
-#pragma unroll
-  for (int b = 0; b < RB; ++b) {
-    const int mc = min(16 * b + c, M - 1);
-    x_rd[b] = mc * C4 + (kb ^ (mc & (C4 - 1)));
-  }
+  // read slot of step 0 (row c, rows past M repeat row M - 1); step st adds
+  // 4 st inside the XOR.  Slice s of row m sits at slot C4 m + (s ^ (m % C4)).
+  const int mc = min(c, M - 1);
+  const int x_rd = mc * C4 + (kb ^ (mc & (C4 - 1)));
   const uint32_t magic = dec_magic_vgpr<DT>();
   const F ones = __builtin_bit_cast(F, u32x4{Num::ONES, Num::ONES, Num::ONES, Num::ONES});
 
@@ -359,13 +354,13 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  f32x4 acc[RB][VEC];
-  f32x4 xs[RB];
-  float tot[VEC][RB * R];
+  f32x4 acc[VEC];
+  f32x4 xs;
+  float tot[VEC][R];
 #pragma unroll
   for (int j = 0; j < VEC; ++j)
 #pragma unroll
-    for (int r = 0; r < RB * R; ++r) tot[j][r] = 0.0f;
+    for (int r = 0; r < R; ++r) tot[j][r] = 0.0f;
 
   auto compute_chunk = [&](const Chunk& ch) {
     if constexpr (ONE) {
@@ -389,25 +384,17 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
 #pragma unroll
       for (int i = 0; i < GS; ++i) {
         const int st = p * GS + i;
-        F xa[RB];
-        if constexpr (ONE) {
-          xa[0] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(xl + (wv * 64 + st * 4 + kb) * 4));
-        } else {
-#pragma unroll
-          for (int b = 0; b < RB; ++b)
-            xa[b] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(
-                                              xl + (wv * MX * C4 + (x_rd[b] ^ (4 * st))) * 4));
-        }
+        F xa;
+        if constexpr (ONE)
+          xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(xl + (wv * 64 + st * 4 + kb) * 4));
+        else
+          xa = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(xl + (wv * MX * C4 + (x_rd ^ (4 * st))) * 4));
 #pragma unroll
         for (int j = 0; j < VEC; ++j) {
           const F bv = __builtin_bit_cast(F, Num::bvals(DecW<VEC>::get(ch.w[st], j), magic));
-#pragma unroll
-          for (int b = 0; b < RB; ++b)
-            acc[b][j] = Mfma<DT>::m16(xa[b], bv, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[b][j]);
+          acc[j] = Mfma<DT>::m16(xa, bv, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[j]);
         }
-#pragma unroll
-        for (int b = 0; b < RB; ++b)
-          xs[b] = Mfma<DT>::m16(xa[b], ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs[b]);
+        xs = Mfma<DT>::m16(xa, ones, i == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : xs);
       }
       // QS * sum x (q - z) = acc - (OFF + QS z) xs, one fma per accumulator
       // (OFF + QS z is exact for the integer zero points of the format);
@@ -419,14 +406,12 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
         sc[j] = ch.s[p].get(j);
       }
 #pragma unroll
-      for (int b = 0; b < RB; ++b)
+      for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int j = 0; j < VEC; ++j) {
-            const float u = __builtin_fmaf(-zc[j], xs[b][r], acc[b][j][r]);
-            tot[j][b * R + r] = __builtin_fmaf(sc[j], u, tot[j][b * R + r]);
-          }
+        for (int j = 0; j < VEC; ++j) {
+          const float u = __builtin_fmaf(-zc[j], xs[r], acc[j][r]);
+          tot[j][r] = __builtin_fmaf(sc[j], u, tot[j][r]);
+        }
     }
     __builtin_amdgcn_wave_barrier();  // slots are rewritten by the next chunk
   };
@@ -453,8 +438,8 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   const int rstride = ONE ? M * TN : MX * C4 * 4;
   if (ONE ? kb == 0 : true) {
 #pragma unroll
-    for (int r = 0; r < RB * R; ++r) {
-      const int m = ONE ? 0 : (r / R) * 16 + kb * 4 + r % R;
+    for (int r = 0; r < R; ++r) {
+      const int m = ONE ? 0 : kb * 4 + r;
       if (m < M) {
 #pragma unroll
         for (int j = 0; j < VEC; ++j) rbase[wv * rstride + m * TN + VEC * c + j] = tot[j][r];
@@ -523,14 +508,6 @@ constexpr int one_lds(int mr) {
   return one_red_offset(mr) + (mr >= 8 ? 0 : kOneWaves * mr * 128 * (int)sizeof(float));
 }
 
-// K-split tile (M == 1): wave 0 sums the per-wave partials of the tile's 128
-// columns (two per lane, same fixed order as above) and publishes them as fp32
-// partials with device-coherent stores (sc1: no device-wide cache write-back
-// is needed to make them visible); once they have completed it bumps the
-// tile's arrival counter (a relaxed device-scope atomic).  The last of the
-// tile's ks workgroups reads all parts back with device-coherent loads, sums
-// them in part order and writes y, then leaves the counter at zero.  Every
-// output bit is a function of the inputs only.
 constexpr int kMaxKSplit = 8;  // K parts of one M == 1 column tile
 constexpr int kMaxRowSlices = 4;  // 16-row slices of one problem (M <= 64)
 
@@ -886,9 +863,7 @@ __global__ __launch_bounds__(kDecThreads) void dec_kernel(DecGroupedArgs g) {
   // !ONE: [activation areas: 8 waves x MX x 4C x 16 B], reused for the reduction
   uint32_t* xl = reinterpret_cast<uint32_t*>(dec_smem);
   float* red = dec_smem + kDecWaves * 64 * 4;
-  if constexpr (MX == 32) {  // the host gives 32-row launches 64-column tiles only
-    dec_tile<DT, 4, ONE, (GS < 4 ? GS : 4), MX>(a, tile, red, xl);
-  } else if constexpr (MX == 16) {  // problems of more rows in 16-row slices
+  if constexpr (MX == 16) {  // problems of more rows in 16-row slices
     int st = tile;
     const DecArgs as = dec_row_slice(a, st);
     if (as.vec == 4)
@@ -965,7 +940,7 @@ int one_ksplit(int64_t K, int G, int level, int64_t N) {
 bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int64_t M,
               DecPlan& dp, const int64_t* mrows = nullptr) {
   dp = DecPlan{};
-  if (count < 1 || count > W4_MAX_GROUPED || M < 1 || M > 32) return false;
+  if (count < 1 || count > W4_MAX_GROUPED || M < 1 || M > 16) return false;
   struct Item {
     int idx;
     int vec, cfg, tile_n;
@@ -1032,9 +1007,6 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     const w4a16_problem& q = problems[i];
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     int vec = 1, cfg = 0, tn = 16, ks = 1;
-    // with group 32 the per-step correction of 32 rows costs more than the
-    // split-K path saves (7-launch block at M = 32: 82.0 against 76.5 us)
-    if (M > 16 && q.group_size < 64) return false;
     if (cu_tiles) {
       vec = 4;
       ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : 1;
@@ -1044,8 +1016,6 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
                       : (q.K <= 8192 ? w4::kCfgT32 : w4::kCfgT32Ring);
     } else if (q.N % 4 == 0 && qa % 16 == 0 && sa % 8 == 0 && za % 8 == 0 && q.K <= 4096) {
       vec = 4, tn = 64;
-    } else if (M > 16) {
-      return false;  // 32-row launches: 64-column tiles only
     } else if (q.N % 2 == 0 && qa % 8 == 0 && sa % 4 == 0 && za % 4 == 0) {
       vec = 2, tn = 32;
     }
@@ -1110,7 +1080,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     // 10.9 us with 8 rows against 12.2 / 12.4 us with 4, while launches of at
     // most one workgroup per CU are 6 % slower with 8); the rows fed to the
     // MFMA, and so every output bit, do not depend on it
-    dp.mx = (M <= 4 && wgs <= device_cu_count()) ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : 32;
+    dp.mx = (M <= 4 && wgs <= device_cu_count()) ? 4 : M <= 8 ? 8 : 16;
     bool narrow = false;  // a tile of vec < 4 has chunks of 8 steps (32 slices per row)
     for (int s = 0; s < count; ++s) narrow = narrow || dp.g.prob[s].vec < 4;
     // ONE: activation slots + reduction; M > 1: activation areas (at most
@@ -1166,10 +1136,8 @@ void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
     dec_launch_generic<DT, false, 4>(dp, st);
   else if (dp.mx == 8)
     dec_launch_generic<DT, false, 8>(dp, st);
-  else if (dp.mx == 16)
-    dec_launch_generic<DT, false, 16>(dp, st);
   else
-    dec_launch_generic<DT, false, 32>(dp, st);
+    dec_launch_generic<DT, false, 16>(dp, st);
 }
 
 }  // namespace

@@ -176,9 +176,9 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
   const int rc = check_grouped(problems, count, M);
   if (rc != W4_OK) return rc;
   if (M > kDecodeM) {
-    // up to 32 rows, one decode launch when every problem fits its 64-column
-    // tiles; else one launch when the products share their activation matrix,
-    // else one w4a16_gemm per problem, in order, on the stream (x rows of K
+    // up to 64 rows, one decode launch with every problem in 16-row slices;
+    // else one launch when the products share their activation matrix, else
+    // one w4a16_gemm per problem, in order, on the stream (x rows of K
     // elements)
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (M <= kSliceM) {
