@@ -5,9 +5,9 @@ reference (int4_triton/gemm.py:223-317):
 
   * M <= 16:       decode kernel, one launch, no workspace (group sizes >= 32
                    and dense rows; else split-K with a fixed-order reduce);
-                   up to M = 32 for operands that fit its 64-column tiles
-                   (K <= 4096, N % 4 == 0, group >= 64);
-  * 17 <= M <= 64: otherwise split-K with fp32 partials and a fixed-order
+  * 17 <= M <= 64: the same decode kernel in one launch, the rows cut into
+                   slices of 16 (dense, 16-byte aligned rows, group >= 32);
+                   otherwise split-K with fp32 partials and a fixed-order
                    reduce kernel;
   * M > 64:        tiled MFMA GEMM writing the output dtype directly, split
                    over K (same partials and reduce) for shapes with too few
@@ -157,11 +157,11 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
     """Several independent products ``xs[i] @ W_i^T``, fused into one launch.
 
     ``weights[i]`` is a ``(qweight, scales, zeros)`` triple.  All ``xs[i]`` share
-    dtype and the leading size M.  For M <= 16 every problem runs in one decode
-    launch, up to M = 32 too when every problem has K <= 4096, N % 4 == 0 and G >= 64;
-    for larger M, products of one shared activation tensor (q/k/v,
-    gate/up: pass the same tensor) run as one prefill launch when the library's
-    plan allows it, else one launch each.  This fuses the per-linear launches
+    dtype and the leading size M.  For M <= 64 every problem runs in one decode
+    launch (rows in slices of 16 above M = 16; group sizes >= 32); otherwise
+    products of one shared activation tensor (q/k/v, gate/up: pass the same
+    tensor) run as one prefill launch when the library's plan allows it, else
+    one launch each.  This fuses the per-linear launches
     of a transformer block; it has no single counterpart in the reference.
     """
     assert 1 <= len(xs) == len(weights) <= _lib.MAX_GROUPED
