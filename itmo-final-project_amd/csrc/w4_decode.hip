@@ -69,6 +69,10 @@ struct DecArgs {
   // rows [16 s, 16 s + 16), s = t / col_tiles (see dec_row_slice)
   int slices;
   int col_tiles;
+  // sixteen rows, ksplit > 1: per column tile one arrival counter (zero on
+  // entry and left zero) and ksplit partial tiles of 16 x 64 floats
+  unsigned* cnt;
+  float* part;
 };
 
 // The column tile and row slice of tile `tile` of a 16-row problem: a copy of
@@ -86,6 +90,10 @@ __device__ __forceinline__ DecArgs dec_row_slice(const DecArgs& g, int& tile) {
     a.y = g.y + (int64_t)r0 * g.ldy;
     a.M = min(16, g.M - r0);
     a.x_bytes = (uint32_t)(((int64_t)(a.M - 1) * g.sxm + g.K) * 2);
+    if (g.ksplit > 1) {
+      a.cnt = g.cnt + (int64_t)s * (g.col_tiles / g.ksplit);
+      a.part = g.part + (int64_t)s * g.col_tiles * (16 * 64);
+    }
   }
   return a;
 }
@@ -619,8 +627,9 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     part = lane >= 40 ? 1 : 0;
   }
   const int N = a.N, K = a.K, M = MR == 1 ? 1 : a.M;
-  // K split (M == 1): column tile ct, part kp of ks, steps [s0, s0 + S)
-  const int ks = MR == 1 ? a.ksplit : 1;
+  // K split (M == 1, and sixteen rows): column tile ct, part kp of ks,
+  // steps [s0, s0 + S)
+  const int ks = MR == 1 || MR == 16 ? a.ksplit : 1;
   const int ct = ks > 1 ? tile / ks : tile;
   const int kp = tile - ct * ks;
   const int n0 = ct * TW;
@@ -777,6 +786,48 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       return;
     }
   }
+  if constexpr (MR == 16) {
+    if (ks > 1) {
+      // Sixteen rows, K split: each part publishes its 16 x 64 partial tile
+      // with device-coherent stores (sc1: written through to the point all
+      // XCDs read from), waits until they have completed and bumps the
+      // tile's counter; the part that arrives last reads the others' tiles
+      // with device-coherent loads, sums all parts in part order (so the
+      // result does not depend on which part is last) and writes y, then
+      // leaves the counter at zero.  Thread tid owns element tid of the
+      // tile (MR * TW == kOneThreads).
+      static_assert(MR * TW == kOneThreads, "one tile element per thread");
+      const int m = tid / TW, nl = tid - m * TW;
+      float pv[kOneWaves];
+#pragma unroll
+      for (int w = 0; w < kOneWaves; ++w) pv[w] = red[w * RSTR + m * RROW + nl];
+      float v = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kOneWaves; ++w) v += pv[w];
+      float* const tiles = a.part + (int64_t)ct * ks * (MR * TW);
+      __hip_atomic_store(tiles + kp * (MR * TW) + tid, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();  // every partial of this part has completed; red is no longer read
+      unsigned* const arrived = reinterpret_cast<unsigned*>(lds);
+      if (tid == 0) *arrived = __hip_atomic_fetch_add(a.cnt + ct, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (*arrived != (unsigned)(ks - 1)) return;
+      if (tid == 0) __hip_atomic_store(a.cnt + ct, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      float other[kMaxKSplit];
+#pragma unroll
+      for (int p = 0; p < kMaxKSplit; ++p)
+        other[p] = (p < ks && p != kp)
+                       ? __hip_atomic_load(tiles + p * (MR * TW) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : v;
+      float sum = 0.0f;
+#pragma unroll
+      for (int p = 0; p < kMaxKSplit; ++p)
+        if (p < ks) sum += other[p];
+      const int n = n0 + nl;
+      if (m < M && n < N) a.y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(sum * (1.0f / Num::QS));
+      return;
+    }
+  }
   if (tid < MR * TW) {
     const int m = tid / TW, nl = tid - m * TW;
     const int n = n0 + nl;
@@ -903,7 +954,33 @@ struct DecPlan {
   // into the workspace's counter area
   int64_t pair_words;
   int64_t pair_off[W4_MAX_GROUPED];
+  // K-split problems (sixteen rows): arrival counters (32-bit word offsets
+  // into the counter area) and partial tiles (float offsets into the scratch)
+  int64_t cnt_words, part_floats;
+  int64_t cnt_off[W4_MAX_GROUPED], part_off[W4_MAX_GROUPED];
 };
+
+// Sixteen rows (9 <= M <= 64), one workgroup per CU: the 64-column tiles
+// hold K <= 4096 in one round, so a longer K (down_proj, 8192) is cut into
+// ks parts (a power of two, whole groups and 256-k rounds), each part a
+// workgroup of 64 columns x K / ks, combined by the last part to arrive
+// (dec_tile_one).  Against the generic kernel's 32-column tiles over all of
+// K (128-byte pieces of the qweight rows), this reads 256-byte pieces with
+// all loads of a wave in flight at once.  Returns 1 for K <= 4096, 0 when no
+// such split exists.
+// `deeper` halves the parts again that many times while they stay whole
+// groups and rounds: a lone down_proj at M = 16 has only 32 column tiles.
+int sixteen_ksplit(int64_t K, int G, int deeper = 0) {
+  if (K <= 4096) return 1;
+  auto ok = [&](int k) {
+    return k <= w4::kMaxKSplit && K % k == 0 && (K / k) % 256 == 0 && (K / k) % G == 0;
+  };
+  int ks = 2;
+  while (K / ks > 4096) ks *= 2;
+  if (!ok(ks)) return 0;
+  for (int d = 0; d < deeper && ok(2 * ks); ++d) ks *= 2;
+  return ks;
+}
 
 // M == 1, one workgroup per CU: problems with K > 4096 are cut into ksplit
 // K parts of at most 4096 (ksplit a power of two) on 64-column tiles, i.e.
@@ -938,7 +1015,7 @@ int one_ksplit(int64_t K, int G, int level, int64_t N) {
 // group size < 32, mixed group-size classes, misaligned or non-dense
 // activations, or offsets past 2 GiB.
 bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int64_t M,
-              DecPlan& dp, const int64_t* mrows = nullptr) {
+              DecPlan& dp, const int64_t* mrows = nullptr, bool split16 = false) {
   dp = DecPlan{};
   if (count < 1 || count > W4_MAX_GROUPED || M < 1 || M > 16) return false;
   struct Item {
@@ -966,8 +1043,8 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     if (ldy != nullptr && ldy[i] < q.N) return false;
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
-    if (M > 1) cu_tiles = cu_tiles && q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096);
-    if (M > 8) cu_tiles = cu_tiles && q.K <= 4096;
+    if (M > 1 && M <= 8) cu_tiles = cu_tiles && q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096);
+    if (M > 8) cu_tiles = cu_tiles && (q.K <= 4096 || (split16 && sixteen_ksplit(q.K, q.group_size) > 1));
   }
   const int G = problems[0].group_size;
   // M == 1 tile width: about 128 KB of packed weights per workgroup (128
@@ -994,6 +1071,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     return (q.N + tn - 1) / tn;
   };
   int level = 0;
+  int deeper = 0;  // sixteen rows: extra halvings of the K parts
   if (cu_tiles) {
     const int cus = device_cu_count();
     while (level < 2) {
@@ -1002,6 +1080,19 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
       if (next > cus) break;
       ++level;
     }
+    if (M > 8) {
+      // split K deeper while the launch still fits one workgroup per CU
+      auto tiles16 = [&](int d) {
+        int64_t t = 0;
+        for (int i = 0; i < count; ++i) {
+          const w4a16_problem& q = problems[i];
+          const int64_t Mi = mrows != nullptr ? mrows[i] : M;
+          t += (q.N + 63) / 64 * sixteen_ksplit(q.K, q.group_size, d) * ((Mi + M - 1) / M);
+        }
+        return t;
+      };
+      while (deeper < 2 && tiles16(deeper + 1) > tiles16(deeper) && tiles16(deeper + 1) <= cus) ++deeper;
+    }
   }
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
@@ -1009,7 +1100,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int vec = 1, cfg = 0, tn = 16, ks = 1;
     if (cu_tiles) {
       vec = 4;
-      ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : 1;
+      ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : M > 8 ? sixteen_ksplit(q.K, G, deeper) : 1;
       tn = ks > 1 ? 64 : one_width(q.K, level);
       cfg = tn == 128 ? w4::kCfgT128
           : tn == 64  ? (q.K / ks <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring)
@@ -1055,7 +1146,15 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     a.pair = nullptr;
     a.slices = it.slices;
     a.col_tiles = (int)(it.tiles / it.slices);
-    if (it.ks > 1) {
+    a.cnt = nullptr;
+    a.part = nullptr;
+    if (it.ks > 1 && M > 1) {
+      dp.cnt_off[s] = dp.cnt_words;
+      dp.part_off[s] = dp.part_floats;
+      dp.cnt_words += it.tiles / it.ks;
+      dp.part_floats += it.tiles * 16 * 64;
+    }
+    if (it.ks > 1 && M == 1) {
       dp.pair_off[s] = dp.pair_words;
       dp.pair_words += (it.tiles / it.ks) * (it.ks - 1) * it.tile_n;
     }
@@ -1142,6 +1241,22 @@ void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
 
 }  // namespace
 
+// The sixteen-row K split is used when its counters fit the counter area and
+// its workgroups one per CU (a grouped launch that would need a second round
+// of workgroups stays on the generic kernel): a function of the shapes only,
+// so a call without the workspace it needs fails (W4_ERR_WORKSPACE) instead
+// of taking another summation order.
+bool split16_shape_ok(const DecPlan& dp) {
+  return dp.cnt_words * 4 <= W4_WORKSPACE_COUNTER_BYTES && dp.wgs <= device_cu_count();
+}
+
+bool dec_plan_final(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int64_t M,
+                    DecPlan& dp, const int64_t* mrows) {
+  if (!dec_plan(problems, sxm, ldy, count, M, dp, mrows, true)) return false;
+  if (dp.cnt_words > 0 && !split16_shape_ok(dp)) return dec_plan(problems, sxm, ldy, count, M, dp, mrows, false);
+  return true;
+}
+
 // Factored decode launch (see the top of this file).  Returns
 // W4_ERR_UNSUPPORTED, with nothing launched and no error message, when the
 // problems need the general kernels.  sxm: activation row strides, ldy: output
@@ -1151,9 +1266,20 @@ int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const in
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
                      hipStream_t st, const int64_t* mrows) {
   DecPlan dp;
-  if (!dec_plan(problems, sxm, ldy, count, M, dp, mrows)) return W4_ERR_UNSUPPORTED;
-  (void)scratch;
-  (void)scratch_bytes;
+  if (!dec_plan_final(problems, sxm, ldy, count, M, dp, mrows)) return W4_ERR_UNSUPPORTED;
+  if (dp.cnt_words > 0) {
+    const size_t need = (size_t)dp.part_floats * 4;
+    if (counters == nullptr || scratch == nullptr || scratch_bytes < need)
+      return fail(W4_ERR_WORKSPACE, "w4a16 decode: a workspace of %zu bytes is required",
+                  (size_t)W4_WORKSPACE_COUNTER_BYTES + need);
+    for (int s = 0; s < dp.g.count; ++s) {
+      w4::DecArgs& a = dp.g.prob[s];
+      if (a.ksplit > 1) {
+        a.cnt = counters + dp.cnt_off[s];
+        a.part = static_cast<float*>(scratch) + dp.part_off[s];
+      }
+    }
+  }
   if (dp.pair_words > 0) {
     // K-split problems: pairing words in the workspace's counter area
     if (dp.pair_words * 8 > W4_WORKSPACE_COUNTER_BYTES) return W4_ERR_UNSUPPORTED;
@@ -1177,9 +1303,24 @@ int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const in
 // kernels do not take them or split nothing.  Pointers are only used for
 // their alignment, so callers without buffers may pass 256-byte-aligned
 // stand-ins.
-size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M) {
+size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M,
+                                 const int64_t* mrows) {
   DecPlan dp;
-  if (!dec_plan(problems, sxm, nullptr, count, M, dp)) return 0;
+  if (!dec_plan_final(problems, sxm, nullptr, count, M, dp, mrows)) return 0;
+  if (dp.cnt_words > 0) return W4_WORKSPACE_COUNTER_BYTES + (size_t)dp.part_floats * 4;
   if (dp.pair_words == 0 || dp.pair_words * 8 > W4_WORKSPACE_COUNTER_BYTES) return 0;
   return W4_WORKSPACE_COUNTER_BYTES;
+}
+
+// Workspace bytes of one product's decode launch (w4a16_gemm: M <= 16 as is,
+// 17 <= M <= 64 as 16-row slices), for dense aligned operands (stand-ins).
+size_t w4_decode_single_workspace_bytes(int64_t M, int64_t N, int64_t K, int G) {
+  static char aligned_stand_in[256] __attribute__((aligned(256)));
+  const w4a16_problem q{aligned_stand_in, reinterpret_cast<const int32_t*>(aligned_stand_in),
+                        reinterpret_cast<const uint16_t*>(aligned_stand_in),
+                        reinterpret_cast<const uint16_t*>(aligned_stand_in), aligned_stand_in, N, K, G, 0};
+  const int64_t sx = K;
+  if (M <= 16) return w4_decode_workspace_bytes(&q, &sx, 1, M, nullptr);
+  if (M > 16 * w4::kMaxRowSlices) return 0;
+  return w4_decode_workspace_bytes(&q, &sx, 1, 16, &M);
 }

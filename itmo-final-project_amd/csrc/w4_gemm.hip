@@ -41,7 +41,9 @@ static constexpr int64_t kSliceM = 64;
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
                      hipStream_t st, const int64_t* mrows = nullptr);
-size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
+size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M,
+                                 const int64_t* mrows = nullptr);
+size_t w4_decode_single_workspace_bytes(int64_t M, int64_t N, int64_t K, int G);
 
 // Every workspace starts with a W4_WORKSPACE_COUNTER_BYTES area of per-tile
 // arrival counters (zero before first use, left zero by every call), then
@@ -67,6 +69,12 @@ extern "C" size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int gro
     const size_t c = w4_prefill_workspace_bytes(M, N, K);
     scratch = a > b ? a : b;
     scratch = scratch > c ? scratch : c;
+  }
+  if (M <= kSliceM) {
+    // the sixteen-row decode kernel's K split (partial tiles)
+    const size_t d = w4_decode_single_workspace_bytes(M, N, K, group_size);
+    if (d > W4_WORKSPACE_COUNTER_BYTES && d - W4_WORKSPACE_COUNTER_BYTES > scratch)
+      scratch = d - W4_WORKSPACE_COUNTER_BYTES;
   }
   return scratch > 0 ? W4_WORKSPACE_COUNTER_BYTES + scratch : 0;
 }
@@ -150,11 +158,19 @@ static int check_grouped(const w4a16_problem* problems, int count, int64_t M) {
 extern "C" size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, int64_t M) {
   clear_error();
   if (check_grouped(problems, count, M) != W4_OK) return 0;
-  if (M > kDecodeM) {  // room for the separate launches that may replace the shared one
+  if (M > kDecodeM) {
+    // the decode launch's K split (16-row slices), or room for the separate
+    // launches that may replace a shared-activation launch
     size_t most = 0;
     for (int i = 0; i < count; ++i) {
       const size_t b = w4a16_workspace_bytes(M, problems[i].N, problems[i].K, problems[i].group_size);
       most = b > most ? b : most;
+    }
+    if (M <= kSliceM) {
+      int64_t sxm[W4_MAX_GROUPED], mr[W4_MAX_GROUPED];
+      for (int i = 0; i < count; ++i) sxm[i] = problems[i].K, mr[i] = M;
+      const size_t d = w4_decode_workspace_bytes(problems, sxm, count, kDecodeM, mr);
+      most = d > most ? d : most;
     }
     return most;
   }
@@ -163,9 +179,9 @@ extern "C" size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, i
   int64_t sxm[W4_MAX_GROUPED];
   for (int i = 0; i < count; ++i) sxm[i] = problems[i].K;
   const int64_t grp = w4_gemv_grouped_scratch_bytes(problems, count, M);
-  const size_t dec = w4_decode_workspace_bytes(problems, sxm, count, M);  // counter area only
-  if (grp > 0) return W4_WORKSPACE_COUNTER_BYTES + (size_t)grp;
-  return dec;
+  const size_t dec = w4_decode_workspace_bytes(problems, sxm, count, M);
+  const size_t g = grp > 0 ? W4_WORKSPACE_COUNTER_BYTES + (size_t)grp : 0;
+  return g > dec ? g : dec;
 }
 
 extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int x_dtype, int64_t M,
@@ -184,8 +200,12 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
     if (M <= kSliceM) {
       int64_t sxm[W4_MAX_GROUPED], mr[W4_MAX_GROUPED];
       for (int i = 0; i < count; ++i) sxm[i] = problems[i].K, mr[i] = M;
-      const int drc =
-          w4_decode_launch(problems, sxm, nullptr, count, x_dtype, kDecodeM, nullptr, nullptr, 0, st, mr);
+      unsigned* counters;
+      void* scratch;
+      size_t scratch_bytes;
+      split_workspace(workspace, workspace_bytes, &counters, &scratch, &scratch_bytes);
+      const int drc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, kDecodeM, counters, scratch,
+                                       scratch_bytes, st, mr);
       if (drc != W4_ERR_UNSUPPORTED) return drc;
     }
     const int grc = w4_prefill_grouped_launch(problems, count, x_dtype, M, st);

@@ -485,7 +485,8 @@ bool plan_grouped(const w4a16_problem* problems, int count, int64_t M, GroupedPl
 // Scratch bytes (past the workspace's counter area) of the single-problem
 // paths.  M == 1 runs as a one-problem grouped launch (partials finished
 // in-kernel); 2 <= M <= 16 writes fp32 partials for the reduce kernel.
-size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
+size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M,
+                                 const int64_t* mrows = nullptr);
 
 size_t w4_gemv_workspace_bytes(int64_t M, int64_t N, int64_t K, int G) {
   if (M == 1) {
@@ -522,7 +523,6 @@ int w4_skinny_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
                      hipStream_t st, const int64_t* mrows = nullptr);
-size_t w4_decode_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
 
 int w4_gemv_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
                    const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, void* y, int64_t ldy,
