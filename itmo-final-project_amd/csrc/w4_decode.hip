@@ -69,8 +69,9 @@ struct DecArgs {
   // rows [16 s, 16 s + 16), s = t / col_tiles (see dec_row_slice)
   int slices;
   int col_tiles;
-  // sixteen rows, ksplit > 1: per column tile one arrival counter (zero on
-  // entry and left zero) and ksplit partial tiles of 16 x 64 floats
+  // M > 1, ksplit > 1: per column tile one arrival counter (zero on entry
+  // and left zero) and ksplit partial tiles of MR x 64 floats (MR = the
+  // launch's row count: 4, 8 or 16)
   unsigned* cnt;
   float* part;
 };
@@ -627,9 +628,9 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     part = lane >= 40 ? 1 : 0;
   }
   const int N = a.N, K = a.K, M = MR == 1 ? 1 : a.M;
-  // K split (M == 1, and sixteen rows): column tile ct, part kp of ks,
+  // K split (64-column tiles only when M > 1): column tile ct, part kp of ks,
   // steps [s0, s0 + S)
-  const int ks = MR == 1 || MR == 16 ? a.ksplit : 1;
+  const int ks = MR == 1 || TW == 64 ? a.ksplit : 1;
   const int ct = ks > 1 ? tile / ks : tile;
   const int kp = tile - ct * ks;
   const int n0 = ct * TW;
@@ -786,26 +787,29 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       return;
     }
   }
-  if constexpr (MR == 16) {
+  if constexpr (MR > 1 && TW == 64) {
     if (ks > 1) {
-      // Sixteen rows, K split: each part publishes its 16 x 64 partial tile
+      // Several rows, K split: each part publishes its MR x 64 partial tile
       // with device-coherent stores (sc1: written through to the point all
       // XCDs read from), waits until they have completed and bumps the
       // tile's counter; the part that arrives last reads the others' tiles
       // with device-coherent loads, sums all parts in part order (so the
       // result does not depend on which part is last) and writes y, then
-      // leaves the counter at zero.  Thread tid owns element tid of the
-      // tile (MR * TW == kOneThreads).
-      static_assert(MR * TW == kOneThreads, "one tile element per thread");
+      // leaves the counter at zero.  Thread tid < MR * TW owns element tid
+      // of the tile.
+      constexpr int E = MR * TW;
+      static_assert(E <= kOneThreads, "one tile element per thread");
       const int m = tid / TW, nl = tid - m * TW;
-      float pv[kOneWaves];
-#pragma unroll
-      for (int w = 0; w < kOneWaves; ++w) pv[w] = red[w * RSTR + m * RROW + nl];
+      float* const tiles = a.part + (int64_t)ct * ks * E;
       float v = 0.0f;
+      if (tid < E) {
+        float pv[kOneWaves];
 #pragma unroll
-      for (int w = 0; w < kOneWaves; ++w) v += pv[w];
-      float* const tiles = a.part + (int64_t)ct * ks * (MR * TW);
-      __hip_atomic_store(tiles + kp * (MR * TW) + tid, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int w = 0; w < kOneWaves; ++w) pv[w] = red[w * RSTR + m * RROW + nl];
+#pragma unroll
+        for (int w = 0; w < kOneWaves; ++w) v += pv[w];
+        __hip_atomic_store(tiles + kp * E + tid, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();  // every partial of this part has completed; red is no longer read
       unsigned* const arrived = reinterpret_cast<unsigned*>(lds);
@@ -813,11 +817,12 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       __syncthreads();
       if (*arrived != (unsigned)(ks - 1)) return;
       if (tid == 0) __hip_atomic_store(a.cnt + ct, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (tid >= E) return;
       float other[kMaxKSplit];
 #pragma unroll
       for (int p = 0; p < kMaxKSplit; ++p)
         other[p] = (p < ks && p != kp)
-                       ? __hip_atomic_load(tiles + p * (MR * TW) + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       ? __hip_atomic_load(tiles + p * E + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                        : v;
       float sum = 0.0f;
 #pragma unroll
@@ -954,20 +959,21 @@ struct DecPlan {
   // into the workspace's counter area
   int64_t pair_words;
   int64_t pair_off[W4_MAX_GROUPED];
-  // K-split problems (sixteen rows): arrival counters (32-bit word offsets
-  // into the counter area) and partial tiles (float offsets into the scratch)
+  // K-split problems (M > 1): arrival counters (32-bit word offsets into the
+  // counter area) and partial tiles (float offsets into the scratch)
   int64_t cnt_words, part_floats;
   int64_t cnt_off[W4_MAX_GROUPED], part_off[W4_MAX_GROUPED];
 };
 
-// Sixteen rows (9 <= M <= 64), one workgroup per CU: the 64-column tiles
+// Several rows (2 <= M <= 64), one workgroup per CU: the 64-column tiles
 // hold K <= 4096 in one round, so a longer K (down_proj, 8192) is cut into
 // ks parts (a power of two, whole groups and 256-k rounds), each part a
 // workgroup of 64 columns x K / ks, combined by the last part to arrive
-// (dec_tile_one).  Against the generic kernel's 32-column tiles over all of
-// K (128-byte pieces of the qweight rows), this reads 256-byte pieces with
-// all loads of a wave in flight at once.  Returns 1 for K <= 4096, 0 when no
-// such split exists.
+// (dec_tile_one).  Against 32-column tiles over all of K (128-byte pieces
+// of the qweight rows: the four- and eight-row tilings, and the generic
+// kernel beyond eight rows), this reads 256-byte pieces with all loads of a
+// wave in flight at once.  Returns 1 for K <= 4096, 0 when no such split
+// exists.
 // `deeper` halves the parts again that many times while they stay whole
 // groups and rounds: a lone down_proj at M = 16 has only 32 column tiles.
 int sixteen_ksplit(int64_t K, int G, int deeper = 0) {
@@ -1043,8 +1049,10 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     if (ldy != nullptr && ldy[i] < q.N) return false;
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
-    if (M > 1 && M <= 8) cu_tiles = cu_tiles && q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096);
-    if (M > 8) cu_tiles = cu_tiles && (q.K <= 4096 || (split16 && sixteen_ksplit(q.K, q.group_size) > 1));
+    const bool split_ok = split16 && sixteen_ksplit(q.K, q.group_size) > 1;
+    if (M > 1 && M <= 8)
+      cu_tiles = cu_tiles && ((q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096)) || split_ok);
+    if (M > 8) cu_tiles = cu_tiles && (q.K <= 4096 || split_ok);
   }
   const int G = problems[0].group_size;
   // M == 1 tile width: about 128 KB of packed weights per workgroup (128
@@ -1080,18 +1088,30 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
       if (next > cus) break;
       ++level;
     }
-    if (M > 8) {
+    if (M > 1 && split16) {
       // split K deeper while the launch still fits one workgroup per CU
       auto tiles16 = [&](int d) {
         int64_t t = 0;
         for (int i = 0; i < count; ++i) {
           const w4a16_problem& q = problems[i];
           const int64_t Mi = mrows != nullptr ? mrows[i] : M;
-          t += (q.N + 63) / 64 * sixteen_ksplit(q.K, q.group_size, d) * ((Mi + M - 1) / M);
+          const int k = sixteen_ksplit(q.K, q.group_size, d);
+          t += (k > 1 ? (q.N + 63) / 64 * k : tiles_at(q, level)) * ((Mi + M - 1) / M);
         }
         return t;
       };
       while (deeper < 2 && tiles16(deeper + 1) > tiles16(deeper) && tiles16(deeper + 1) <= cus) ++deeper;
+      // up to eight rows, K <= 8192 (group >= 64) also fits the unsplit
+      // 32-column tiling:
+      // split only where the parts spread over more CUs (a lone long-K
+      // product); a launch that is already full (the grouped decoder block)
+      // ran 0.4 us slower with the split's tail at M = 4
+      if (M <= 8 && deeper == 0) {
+        bool needed = false;  // a problem no single-round tiling holds
+        for (int i = 0; i < count; ++i)
+          needed = needed || problems[i].K > 8192 || (problems[i].group_size < 64 && problems[i].K > 4096);
+        split16 = needed;
+      }
     }
   }
   for (int i = 0; i < count; ++i) {
@@ -1100,7 +1120,9 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     int vec = 1, cfg = 0, tn = 16, ks = 1;
     if (cu_tiles) {
       vec = 4;
-      ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : M > 8 ? sixteen_ksplit(q.K, G, deeper) : 1;
+      // (sixteen_ksplit returns 0 where no split exists: those problems stay
+      // whole, on the single-round tilings)
+      ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : split16 ? std::max(1, sixteen_ksplit(q.K, G, deeper)) : 1;
       tn = ks > 1 ? 64 : one_width(q.K, level);
       cfg = tn == 128 ? w4::kCfgT128
           : tn == 64  ? (q.K / ks <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring)
@@ -1149,10 +1171,11 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     a.cnt = nullptr;
     a.part = nullptr;
     if (it.ks > 1 && M > 1) {
+      const int mr = M <= 4 ? 4 : M <= 8 ? 8 : 16;  // rows of the launch's kernel
       dp.cnt_off[s] = dp.cnt_words;
       dp.part_off[s] = dp.part_floats;
       dp.cnt_words += it.tiles / it.ks;
-      dp.part_floats += it.tiles * 16 * 64;
+      dp.part_floats += it.tiles * mr * 64;
     }
     if (it.ks > 1 && M == 1) {
       dp.pair_off[s] = dp.pair_words;
@@ -1241,7 +1264,7 @@ void dec_launch(const DecPlan& dp, int64_t M, hipStream_t st) {
 
 }  // namespace
 
-// The sixteen-row K split is used when its counters fit the counter area and
+// The several-row K split is used when its counters fit the counter area and
 // its workgroups one per CU (a grouped launch that would need a second round
 // of workgroups stays on the generic kernel): a function of the shapes only,
 // so a call without the workspace it needs fails (W4_ERR_WORKSPACE) instead

@@ -75,6 +75,38 @@ def test_c_abi_rejects_bad_gemm_arguments(lib):
         assert n == 0 or n > 65536
 
 
+def test_workspace_queries_over_regime_boundaries(lib):
+    """The size queries run the launch planners on the host only: a sweep over
+    the regime boundaries (M around 1 / 4 / 8 / 16 / 64, K around 4096 and
+    8192, K without a whole-round split such as 4352, every group size)
+    answers without error, and every non-zero size covers the counter area."""
+    import ctypes
+
+    count = 0
+    for M in (1, 2, 3, 4, 5, 8, 9, 13, 16, 17, 24, 33, 40, 64, 65, 128):
+        for N in (8, 72, 200, 2048, 8192):
+            for K in (256, 2048, 4096, 4352, 6144, 8192, 12288, 14336, 16384):
+                for G in (32, 64, 128, 256, 1024):
+                    if K % G:
+                        continue
+                    n = lib.w4a16_workspace_bytes(M, N, K, G)
+                    assert n == 0 or n > 65536
+                    count += 1
+    assert count > 2000
+    # grouped queries on 256-byte aligned stand-ins (only the alignment is read)
+    buf = ctypes.create_string_buffer(512)
+    base = (ctypes.addressof(buf) + 255) // 256 * 256
+    shapes = [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)]
+    for M in (1, 3, 8, 12, 16, 24, 40, 64, 65):
+        for G in (32, 128):
+            for shp in (shapes, [(300, 4352), (200, 6144)], [(72, 12288)]):
+                probs = (_lib.Problem * len(shp))()
+                for i, (N, K) in enumerate(shp):
+                    probs[i] = _lib.Problem(base, base, base, base, base, N, K, G, 0)
+                n = lib.w4a16_grouped_workspace_bytes(probs, len(shp), M)
+                assert n == 0 or n >= 65536
+
+
 def test_c_abi_rejects_bad_grouped_arguments(lib):
     probs = (_lib.Problem * 1)()
     assert lib.w4a16_gemm_grouped(probs, 0, 0, 1, None, 0, None) == _lib.ERR_INVALID

@@ -365,16 +365,18 @@ def test_decode_ksplit_pairs_repeat(N, K, G):
         assert torch.equal(y.view(torch.int16), grouped_first.view(torch.int16))
 
 
-# sixteen-row decode kernel with K split (K > 4096 at 9 <= M <= 64): parts of
+# several-row decode kernels with K split (K > 4096 at 2 <= M <= 64): parts of
 # 64 columns x K / ks combined by the last part to arrive; partial column
 # tiles, several slices, ks = 2 and 4, every group size; repeated calls with
 # the workspace's scratch poisoned in between must give the same bits (the
 # arrival counters are left at zero, the partial tiles are always rewritten)
-@pytest.mark.parametrize("M,N,K,G", [(9, 200, 6144, 64), (16, 2048, 8192, 128), (16, 2048, 16384, 32),
+@pytest.mark.parametrize("M,N,K,G", [(2, 2048, 8192, 128), (3, 300, 6144, 32), (4, 1024, 16384, 64),
+                                     (6, 2048, 8192, 256), (8, 200, 12288, 128),
+                                     (9, 200, 6144, 64), (16, 2048, 8192, 128), (16, 2048, 16384, 32),
                                      (13, 4096, 14336, 128), (40, 520, 8192, 32), (64, 72, 12288, 128),
                                      (64, 2048, 8192, 64)])
-def test_decode_sixteen_rows_ksplit(M, N, K, G):
-    print(f"[ksplit16] M={M} N={N} K={K} G={G}", flush=True)
+def test_decode_rows_ksplit(M, N, K, G):
+    print(f"[ksplit-rows] M={M} N={N} K={K} G={G}", flush=True)
     qw, s, z = _weights(N, K, G, seed=3 * N + K + G)
     x = randn((M, K), seed=M + K).to(DEV)
     first = int4_hip.w4a16_matmul(x, qw, s, z)
