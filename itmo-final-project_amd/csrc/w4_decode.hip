@@ -1,6 +1,6 @@
 // Decode-shaped W4A16 products (1 <= M <= 16, group size >= 32; up to 64
-// rows as 16-row slices of one launch) for gfx950: one launch, no fp32
-// partials in memory, the dequantization factored out of the K loop.
+// rows as 16-row slices of one launch) for gfx950: one launch, no reduce
+// launch, the dequantization factored out of the K loop.
 //
 // Arithmetic.  For one output column n and one quantization group g,
 //   sum_k x_k (q_k - z) s = s * ( sum_k x_k (OFF + QS q_k) - OFF xs - QS z xs ) / QS
@@ -17,19 +17,25 @@
 // W_hat to the activation dtype first, int4_triton/gemm.py:139,203; both are
 // within the reference's tolerance of the exact product).
 //
-// Work decomposition.  A workgroup owns a column tile of TN = 16*VEC columns
-// over the whole K (no cross-workgroup reduction).  VEC = 4 (256-byte row
-// segments) for K <= 4096, VEC = 2 (128-byte segments, one cache line) for
-// longer K, so a workgroup streams at most 128 KB for K <= 8192.  Its eight
-// waves take contiguous runs of 32-wide K steps and stream them in chunks of
-// C steps, double buffered: the next chunk's weights, activations and
-// scales/zeros are in flight while the current one is computed.  All loads
-// are raw buffer loads; a chunk past the end of a wave's run uses an offset
-// that the hardware range check turns into zeros with no memory traffic, so
-// the load sequence is unconditional.  The per-wave partial tiles are summed
-// through LDS in wave order, so every output bit is fixed.  (M <= 4 with
-// 16-byte aligned weights and N % 8 == 0, K <= 8192: the one-workgroup-per-CU
-// kernel further down, dec_kernel_one, instead.)
+// Two kernels.  dec_kernel_one (further down) takes every launch whose
+// operands are 16-byte aligned with N % 8 == 0: one workgroup of 16 waves per
+// CU-sized tile, all loads of a wave in flight at once, K longer than its
+// single-round tilings cut into K parts combined across workgroups (a pair
+// tree of compare-and-swap words at M = 1, the last part to arrive for more
+// rows).  dec_kernel, the generic kernel, takes the rest:
+//
+// Work decomposition (dec_kernel).  A workgroup owns a column tile of
+// TN = 16*VEC columns over the whole K (no cross-workgroup reduction).
+// VEC = 4 (256-byte row segments) for K <= 4096, VEC = 2 (128-byte segments,
+// one cache line) for longer K, so a workgroup streams at most 128 KB for
+// K <= 8192.  Its eight waves take contiguous runs of 32-wide K steps and
+// stream them in chunks of C steps, double buffered: the next chunk's
+// weights, activations and scales/zeros are in flight while the current one
+// is computed.  All loads are raw buffer loads; a chunk past the end of a
+// wave's run uses an offset that the hardware range check turns into zeros
+// with no memory traffic, so the load sequence is unconditional.  The
+// per-wave partial tiles are summed through LDS in wave order, so every
+// output bit is fixed.
 //
 // Nibble order.  The four dwords built from one packed word hold nibbles
 // (0,4), (1,5), (2,6), (3,7); the activation fragment is permuted to the same
@@ -469,11 +475,12 @@ __device__ __forceinline__ void dec_tile(const DecArgs& a, int tile, float* red,
   }
 }
 
-// ------------------------------------------ M <= 4 path (one workgroup per CU)
+// ------------------------------- dec_kernel_one (one workgroup per CU tile)
 //
-// One workgroup of 16 waves per CU-sized unit of work: a column tile over the
-// whole K of about 128 KB of packed weights, so that the seven linears of a
-// decoder block become about 230 equal workgroups, at most one per CU.  Every
+// One workgroup of 16 waves per CU-sized unit of work: a column tile of about
+// 128 KB of packed weights (over the whole K, or one K part of a long K), so
+// that the seven linears of an M = 1 decoder block become about 230 equal
+// workgroups, at most one per CU.  Every
 // wave issues all loads of its run (a round of NL 128-bit weight loads per
 // lane, plus one load each for the round's activations, scales and zeros)
 // before it waits for any of them; for K <= 8192 a round is the whole run, so
