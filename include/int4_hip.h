@@ -99,11 +99,12 @@ size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
  * stride_xk).  qweight/scales/zeros dense row-major as above.  y: row stride
  * ldy (>= N), unit column stride.  Launch regimes (same boundaries as the
  * reference): M <= 16 (group sizes >= 32) the factored decode kernel in one
- * launch, no workspace; 17 <= M <= 64 with dense rows (unit column stride,
- * 16-byte aligned, row stride a multiple of 8) the same kernel in one launch,
- * the rows cut into slices of 16; other M <= 64 problems (and group sizes
- * < 32) split-K with fp32 partials in `workspace` and a fixed-order reduce
- * kernel; M > 64 tiled
+ * launch; 17 <= M <= 64 with dense rows (unit column stride, 16-byte aligned,
+ * row stride a multiple of 8) the same kernel in one launch, the rows cut
+ * into slices of 16 (in both, a long K is split over workgroups whose fp32
+ * partial tiles, in `workspace`, are summed in part order by the last one to
+ * finish); other M <= 64 problems (and group sizes < 32) split-K with fp32
+ * partials in `workspace` and a fixed-order reduce kernel; M > 64 tiled
  * MFMA GEMM, itself split over K with the same partials-and-reduce scheme
  * when the shape leaves too few tiles to fill the chip.  Every regime is
  * bit-identical run to run.
@@ -147,7 +148,8 @@ size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, i
  *   kernel).  Problems with a long K may be split over several workgroups whose
  *   fp32 partials meet in a fixed order (in `workspace`).
  *   17 <= M <= 64: the same single decode launch, each problem's rows cut into
- *   slices of 16 (group sizes >= 32, 16-byte aligned x).
+ *   slices of 16 (group sizes >= 32, 16-byte aligned x), long K split the same
+ *   way.
  *   Otherwise, M > 16: problems that share one activation matrix (same x pointer, K and
  *   group size; at most 4) run as ONE launch of the prefill kernel (no
  *   split-K, the tiles of all problems side by side) when the library's
