@@ -504,16 +504,32 @@ def main() -> int:
                 if rc != 0:
                     raise RuntimeError(f"w4a16_gemm_grouped failed in the step loop ({rc})")
 
+            blib.w4bench_gate_new.restype = ctypes.c_void_p
+            blib.w4bench_gate_close.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_double]
+            blib.w4bench_gate_open.argtypes = [ctypes.c_void_p]
+            blib.w4bench_gate_state.argtypes = [ctypes.c_void_p]
+            blib.w4bench_gate_free.argtypes = [ctypes.c_void_p]
+            gate = blib.w4bench_gate_new()
+            if not gate:
+                raise RuntimeError("bench: could not allocate the step gate's pinned word")
             c_steps(warm)
             torch.cuda.synchronize()
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            host_spin(2.0)
+            # the gate holds the stream until every timed call is queued, so
+            # the events bracket the GPU's back-to-back execution of the steps
+            # and not the host's latency to issue the first of them
+            if blib.w4bench_gate_close(gate, stream.cuda_stream, 500.0) != 0:
+                raise RuntimeError("bench: step gate launch failed")
             e0.record(stream)
             c_steps(steps)
             e1.record(stream)
+            blib.w4bench_gate_open(gate)
             torch.cuda.synchronize()
+            gate_state = blib.w4bench_gate_state(gate)
+            blib.w4bench_gate_free(gate)
             ms_run = e0.elapsed_time(e1)
-            kern_ms_src = "hip-events-on-launch-stream-over-the-timed-steps (C loop of C-ABI calls)"
+            kern_ms_src = ("hip-events-on-launch-stream-over-the-timed-steps (C loop of C-ABI calls, queued "
+                           "behind a host-opened gate" + ("" if gate_state == 2 else ", gate timed out") + ")")
         else:  # no bench helper: the timed steps as one graph replay
             with torch.cuda.stream(stream):
                 for i in range(warm):

@@ -37,6 +37,16 @@ static constexpr int64_t kDecodeM = 16;
 // Up to this M, dense rows run as row slices of kDecodeM in one decode
 // launch (four slices at most).
 static constexpr int64_t kSliceM = 64;
+// A lone product up to this M with N up to kSliceLoneN takes the row slices
+// too (eight at most): at M = 128 the prefill kernel's plan for these shapes
+// has few tiles and a split-K reduce launch (o_proj 12.5 -> 6.9 us, k_proj
+// 8.9 -> 6.4 us, down_proj 19.2 -> 19.1 us), while for N = 8192 (gate_proj)
+// it was the faster of the two (19.8 against 20.5 us).  Grouped calls above
+// kSliceM keep the shared-activation prefill launch, faster for q/k/v and
+// gate/up together (the 4-call block 69.8 against 79.2 us).
+static constexpr int64_t kSliceLoneM = 128;
+static constexpr int64_t kSliceLoneN = 4096;
+static bool sliced_lone(int64_t M, int64_t N) { return M <= kSliceM || (M <= kSliceLoneM && N <= kSliceLoneN); }
 
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
@@ -70,8 +80,8 @@ extern "C" size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int gro
     scratch = a > b ? a : b;
     scratch = scratch > c ? scratch : c;
   }
-  if (M <= kSliceM) {
-    // the sixteen-row decode kernel's K split (partial tiles)
+  if (sliced_lone(M, N)) {
+    // the several-row decode kernel's K split (partial tiles)
     const size_t d = w4_decode_single_workspace_bytes(M, N, K, group_size);
     if (d > W4_WORKSPACE_COUNTER_BYTES && d - W4_WORKSPACE_COUNTER_BYTES > scratch)
       scratch = d - W4_WORKSPACE_COUNTER_BYTES;
@@ -118,10 +128,10 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
   if (M <= kDecodeM)
     return w4_gemv_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
                           counters, scratch, scratch_bytes, st);
-  if (M <= kSliceM && stride_xk == 1) {
-    // 17 <= M <= 64: the rows as slices of kDecodeM in one decode launch (the
-    // weights are read once per slice, the repeats mostly from L2): no split-K
-    // partials, no reduce launch
+  if (sliced_lone(M, N) && stride_xk == 1) {
+    // 17 <= M <= 64 (and up to 128 for N <= 4096): the rows as slices of
+    // kDecodeM in one decode launch (the weights are read once per slice, the
+    // repeats mostly from L2): no reduce launch
     const w4a16_problem q{x, qweight, scales, zeros, y, N, K, (int32_t)G, 0};
     const int rc = w4_decode_launch(&q, &stride_xm, &ldy, 1, x_dtype, kDecodeM, counters, scratch, scratch_bytes,
                                     st, &M);

@@ -11,7 +11,8 @@ Tolerances (stated per the task's floating-point bar):
 * the reference's own check against the unrounded fp32 W_hat
   (tests/test_kernels.py:60): rtol 2e-2, atol 2e-2 * max |ref|.
 
-The decode regime (M <= 64, group size >= 32, dense activation rows) applies
+The decode regime (M <= 64, or M <= 128 with N <= 4096 for a lone product;
+group size >= 32, dense activation rows) applies
 scales and zero points after the matrix-core sums, so it multiplies by the
 exact fp32 W_hat instead of W_hat rounded to the activation dtype.  Its
 elementwise check is against ref = x @ W_hat_fp32^T with
@@ -32,11 +33,12 @@ DEV = "cuda"
 U_OUT = {torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
 
 
-def _decode(M: int, G: int, N: int = 0, K: int = 1 << 30) -> bool:
-    """True when w4a16_matmul takes the factored decode kernel (dense, aligned
-    rows, group >= 32): M <= 16 directly, 17 <= M <= 64 as slices of at most
-    16 rows in one decode launch."""
-    return G >= 32 and M <= 64
+def _decode(M: int, G: int, N: int = 1 << 30, K: int = 1 << 30) -> bool:
+    """True when a lone w4a16_matmul takes the factored decode kernel (dense,
+    aligned rows, group >= 32): M <= 16 directly, 17 <= M <= 64 as slices of
+    at most 16 rows in one decode launch, and 65 <= M <= 128 the same way
+    when N <= 4096."""
+    return G >= 32 and (M <= 64 or (M <= 128 and N <= 4096))
 
 
 def _check(out: torch.Tensor, x: torch.Tensor, qw, s, z, ref_unrounded: bool = True, exact_w=False):

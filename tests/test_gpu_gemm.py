@@ -212,7 +212,8 @@ def test_prefill_group_sizes_and_partial_tiles(M, G, NK):
     qw, s, z = _weights(N, K, G, seed=200 + G)
     x = randn((M, K), seed=201 + M).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
-    _check(out, x, qw, s, z)
+    # M = 65 with group >= 32 takes the decode kernel's row slices (N <= 4096)
+    _check(out, x, qw, s, z, exact_w=_decode(M, G, N, K))
 
 
 # shapes whose static plan runs 32-row tiles as workgroups of two K halves
@@ -228,7 +229,8 @@ def test_prefill_two_k_halves(M, N, K, dtype):
     assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
 
 
-@pytest.mark.parametrize("M", [128, 512])
+# (M = 128 takes the decode kernel's row slices, with a K split for K = 8192)
+@pytest.mark.parametrize("M", [128, 130, 512])
 @pytest.mark.parametrize("NK", [(512, 2048), (2048, 8192)])
 def test_prefill_split_k_bit_identical(M, NK):
     N, K = NK
@@ -236,7 +238,7 @@ def test_prefill_split_k_bit_identical(M, NK):
     qw, s, z = _weights(N, K, 128, seed=N + M)
     x = randn((M, K), seed=300 + M, dtype=torch.float16).to(DEV)
     out = int4_hip.w4a16_matmul(x, qw, s, z)
-    _check(out, x, qw, s, z, ref_unrounded=False)
+    _check(out, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, 128, N, K))
     for _ in range(2):
         assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
 
@@ -254,8 +256,10 @@ def test_grouped_shared_activation(M, K, Ns, G):
     ws = [_weights(N, K, G, seed=400 + i) for i, N in enumerate(Ns)]
     x = randn((M, K), seed=410 + M).to(DEV)
     # M <= 64: decode launches (exact W_hat) or, where the library's plan
-    # prefers it, one shared-activation prefill launch (W_hat rounded)
-    ew = "either" if M <= 64 else False
+    # prefers it, one shared-activation prefill launch (W_hat rounded); up to
+    # M = 128 the per-problem fallback of mixed inputs may take the decode
+    # kernel's row slices (N <= 4096)
+    ew = "either" if M <= 128 else False
     outs = int4_hip.w4a16_matmul_grouped([x] * len(Ns), ws)
     for (qw, s, z), y in zip(ws, outs):
         _check(y, x, qw, s, z, ref_unrounded=True, exact_w=ew)
