@@ -106,7 +106,9 @@ size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
  * finish); other M <= 64 problems (and group sizes < 32) split-K with fp32
  * partials in `workspace` and a fixed-order reduce kernel; M > 64 tiled
  * MFMA GEMM, itself split over K with the same partials-and-reduce scheme
- * when the shape leaves too few tiles to fill the chip.  Every regime is
+ * when the shape leaves too few tiles to fill the chip, except that
+ * 65 <= M <= 128 with N <= 4096 and dense rows takes the decode kernel's row
+ * slices (up to eight) like 17 <= M <= 64.  Every regime is
  * bit-identical run to run.
  * Replaces: int4_triton/gemm.py:303-309 (w4a16_matmul) and its dispatcher
  * _matmul, :234-300 (kernels :74-157, :171-182, :185-220).

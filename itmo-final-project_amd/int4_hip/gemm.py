@@ -11,7 +11,9 @@ reference (int4_triton/gemm.py:223-317):
                    reduce kernel;
   * M > 64:        tiled MFMA GEMM writing the output dtype directly, split
                    over K (same partials and reduce) for shapes with too few
-                   output tiles to fill the chip.
+                   output tiles to fill the chip; a lone product with
+                   M <= 128 and N <= 4096 on dense rows takes the decode
+                   kernel's row slices instead (up to eight).
 
 The kernels are hand-written HIP (itmo-final-project_amd/csrc); the split
 counts come from a static table inside the library, so results are
