@@ -495,12 +495,13 @@ def main() -> int:
             loop = blib.w4bench_grouped_steps
             loop.restype = ctypes.c_int
             loop.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_int,
-                             ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t,
-                             ctypes.c_void_p]
+                             ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p,
+                             ctypes.c_size_t, ctypes.c_void_p]
 
-            def c_steps(n):
+            def c_steps(first, n):
+                # steps first .. first + n - 1 of the rotation over the weight sets
                 rc = loop(fn_ptr, ctypes.cast(probs, ctypes.c_void_p), ctypes.sizeof(int4_hip._lib.Problem) * nprob,
-                          nprob, nsets, n, int4_hip._lib.DTYPE_BF16, 1, ws_ptr, ws_len, stream.cuda_stream)
+                          nprob, nsets, first, n, int4_hip._lib.DTYPE_BF16, 1, ws_ptr, ws_len, stream.cuda_stream)
                 if rc != 0:
                     raise RuntimeError(f"w4a16_gemm_grouped failed in the step loop ({rc})")
 
@@ -509,33 +510,45 @@ def main() -> int:
             blib.w4bench_gate_open.argtypes = [ctypes.c_void_p]
             blib.w4bench_gate_state.argtypes = [ctypes.c_void_p]
             blib.w4bench_gate_free.argtypes = [ctypes.c_void_p]
+            blib.w4bench_event_new.restype = ctypes.c_void_p
+            blib.w4bench_event_record.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            blib.w4bench_event_ms.restype = ctypes.c_double
+            blib.w4bench_event_ms.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            blib.w4bench_event_free.argtypes = [ctypes.c_void_p]
             gate = blib.w4bench_gate_new()
-            if not gate:
-                raise RuntimeError("bench: could not allocate the step gate's pinned word")
-            c_steps(warm)
+            ev0, ev1 = blib.w4bench_event_new(), blib.w4bench_event_new()
+            if not (gate and ev0 and ev1):
+                raise RuntimeError("bench: could not create the step gate or the timing events")
+            c_steps(0, warm)
             torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             # the gate holds the stream until every timed call is queued, so
             # the events bracket the GPU's back-to-back execution of the steps
-            # and not the host's latency to issue the first of them
+            # and not the host's latency to issue the first of them; the
+            # events are timing-only (no system-scope fence when recorded)
             if blib.w4bench_gate_close(gate, stream.cuda_stream, 500.0) != 0:
                 raise RuntimeError("bench: step gate launch failed")
-            e0.record(stream)
-            c_steps(steps)
-            e1.record(stream)
+            blib.w4bench_event_record(ev0, stream.cuda_stream)
+            c_steps(warm, steps)  # the rotation continues: no set is read twice within 16 steps
+            blib.w4bench_event_record(ev1, stream.cuda_stream)
             blib.w4bench_gate_open(gate)
             torch.cuda.synchronize()
             gate_state = blib.w4bench_gate_state(gate)
+            ms_run = blib.w4bench_event_ms(ev0, ev1)
+            for h in (ev0, ev1):
+                blib.w4bench_event_free(h)
             blib.w4bench_gate_free(gate)
-            ms_run = e0.elapsed_time(e1)
+            if ms_run <= 0:
+                raise RuntimeError("bench: reading the timing events failed")
             kern_ms_src = ("hip-events-on-launch-stream-over-the-timed-steps (C loop of C-ABI calls, queued "
-                           "behind a host-opened gate" + ("" if gate_state == 2 else ", gate timed out") + ")")
+                           "behind a host-opened gate" + ("" if gate_state == 2 else ", gate timed out") +
+                           "; events without the system-scope fence)")
         else:  # no bench helper: the timed steps as one graph replay
             with torch.cuda.stream(stream):
                 for i in range(warm):
                     grouped(i % nsets)()
             torch.cuda.synchronize()
-            g_steps = graph_of(lambda: [grouped(i % nsets)() for i in range(steps)], stream, eager_warmup=False)
+            g_steps = graph_of(lambda: [grouped((warm + i) % nsets)() for i in range(steps)], stream,
+                               eager_warmup=False)
             ms_run = time_graph_once(g_steps, stream)
             del g_steps
             kern_ms_src = "hip-events-on-launch-stream-over-the-timed-steps (one graph replay)"

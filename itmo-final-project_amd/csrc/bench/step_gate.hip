@@ -67,3 +67,29 @@ extern "C" void w4bench_gate_open(void* flag) {
 extern "C" int w4bench_gate_state(void* flag) {
   return (int)__atomic_load_n(static_cast<unsigned*>(flag), __ATOMIC_SEQ_CST);
 }
+
+// Timing-only events for the same region: created with
+// hipEventDisableSystemFence, so recording them does not add the system-scope
+// cache write-back and invalidation of a default event to the region (HIP
+// documents the flag for events that only measure time).  The caller
+// synchronises the device before reading the elapsed time.
+extern "C" void* w4bench_event_new() {
+  hipEvent_t e = nullptr;
+  if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) return nullptr;
+  return static_cast<void*>(e);
+}
+
+extern "C" int w4bench_event_record(void* ev, void* stream) {
+  return (int)hipEventRecord(static_cast<hipEvent_t>(ev), static_cast<hipStream_t>(stream));
+}
+
+// Milliseconds between two recorded events (negative on error).
+extern "C" double w4bench_event_ms(void* e0, void* e1) {
+  float ms = 0.0f;
+  if (hipEventElapsedTime(&ms, static_cast<hipEvent_t>(e0), static_cast<hipEvent_t>(e1)) != hipSuccess) return -1.0;
+  return (double)ms;
+}
+
+extern "C" void w4bench_event_free(void* ev) {
+  if (ev != nullptr) (void)hipEventDestroy(static_cast<hipEvent_t>(ev));
+}
