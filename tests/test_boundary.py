@@ -77,13 +77,13 @@ def test_c_abi_rejects_bad_gemm_arguments(lib):
 
 def test_workspace_queries_over_regime_boundaries(lib):
     """The size queries run the launch planners on the host only: a sweep over
-    the regime boundaries (M around 1 / 4 / 8 / 16 / 64, K around 4096 and
+    the regime boundaries (M around 1 / 4 / 8 / 16 / 64 / 128, K around 4096 and
     8192, K without a whole-round split such as 4352, every group size)
     answers without error, and every non-zero size covers the counter area."""
     import ctypes
 
     count = 0
-    for M in (1, 2, 3, 4, 5, 8, 9, 13, 16, 17, 24, 33, 40, 64, 65, 128):
+    for M in (1, 2, 3, 4, 5, 8, 9, 13, 16, 17, 24, 33, 40, 64, 65, 96, 128, 129):
         for N in (8, 72, 200, 2048, 8192):
             for K in (256, 2048, 4096, 4352, 6144, 8192, 12288, 14336, 16384):
                 for G in (32, 64, 128, 256, 1024):
