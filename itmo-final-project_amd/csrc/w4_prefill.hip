@@ -700,6 +700,217 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
     if (i < g.count && b >= g.wg_start[i]) p = i;
   pf3_tile<DT, NW, SZK, MB, KH>(g.prob[p], b - g.wg_start[p]);
 }
+
+// ---------------------------------------------------------------------------
+// pf5_kernel: 64 x 64 output tiles for products with few tiles (at most one
+// per CU), the weight tile dequantized ONCE per workgroup into LDS.
+//
+// pf3 gives every wave its own 64 columns and dequantizes them in registers
+// for the wave's rows: cheap per MFMA with 128-row tiles, but a shape such as
+// k_proj at M = 2048 (2048 x 512), q_proj at M = 512 (512 x 2048) or gate_proj
+// at M = 128 (128 x 8192) has 256 tiles of 64 x 64 at most, so pf3 runs
+// 32-row tiles whose dequantization is repeated for every 32 rows, or split-K
+// with fp32 partials and a reduce launch.  Here:
+//  * A set of four waves computes the 64 x 64 tile as 2 x 2 blocks of
+//    32 x 32 (one v_mfma_f32_32x32x16 accumulator per wave).  Per 64-k step
+//    the set's 256 threads load the 8 x 64 packed words (two adjacent columns
+//    of one k8 row per thread), dequantize them exactly as pf3 does (fp32
+//    (q - z) * s, one rounding to the activation dtype) and store the bf16 /
+//    fp16 B tile to LDS, column-major with 16-byte chunk (column n, k8 row j)
+//    at slot n * 8 + (j ^ ((n >> 1) & 7)); the activation tile arrives by
+//    direct-to-LDS loads in pf3's swizzled layout, so the A and B fragment
+//    reads (32 rows / columns x one chunk per 16 lanes) hit all banks.
+//  * KP sets (KP = 1, 2 or 4 per workgroup, 4 to 16 waves) run the same tile
+//    over KP contiguous parts of K in lockstep, each with its own LDS area
+//    (3 activation slots, 2 weight buffers: 40 KB); the parts are added
+//    through LDS in part order at the end, so the result is a fixed function
+//    of the inputs (no atomics, no partial-sum buffer, no reduce launch).
+//  * Loads run two steps ahead: one barrier per step, then the step t + 2
+//    loads are issued, step t is multiplied and the words of step t + 1
+//    (landed a step earlier) are dequantized into the other weight buffer.
+//    Every step issues the same number of loads, so "the activations of step
+//    t have landed" is one fixed s_waitcnt vmcnt before the barrier.
+// Measured against pf3's planned launch (bench shapes, G = 128, bf16):
+// k_proj at M = 2048 17.7 -> 13.1 us (KP = 2), q_proj at M = 512 18.7 ->
+// 11.7 us, k_proj at M = 512 11.5 -> 10.5 us, gate_proj at M = 128 18.9 ->
+// 11.7 us (KP = 4); slower where there are more tiles than CUs (q_proj at
+// M = 2048: 33.8 against 25.7 us) or K = 8192 (down_proj at M = 512: 34.8
+// against 33.0 us).  Sub-step software pipelining (pf3's fragment prefetch
+// across the barrier) measured slower here.
+constexpr int PF5_T = 64;                   // tile rows = tile columns
+constexpr int PF5_ASLOT = PF5_T * PF2_BK;  // elements of one activation slot
+constexpr int PF5_BBUF = PF5_T * PF2_BK;   // elements of one weight buffer
+constexpr int PF5_SET = 3 * PF5_ASLOT + 2 * PF5_BBUF;  // elements of one K part's area (40 KB)
+
+template <int DT, int KP>
+__global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
+  typedef typename Act<DT>::frag F;
+  constexpr int XL = PF5_T / 32;  // direct-to-LDS activation loads per thread and step
+  constexpr int NLOAD = 3 + XL;   // loads per thread and step: words, scales, zeros, activations
+  // vmcnt(NLOAD) (only the next step's loads may be outstanding) and lgkmcnt(0)
+  constexpr int WAIT_IMM = (NLOAD & 15) | 0x70 | ((NLOAD >> 4) << 14);
+  static_assert(NLOAD < 16, "vmcnt range");
+  __shared__ __attribute__((aligned(16))) uint16_t lds[KP * PF5_SET];
+  constexpr uint32_t OOB = 0x80000000u;
+
+  const int lane = threadIdx.x & 63;
+  const int kp = KP == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8);  // K part
+  const int tid = threadIdx.x & 255;                                                  // within the part
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  uint16_t* const As = lds + kp * PF5_SET;
+  uint16_t* const Bs = As + 3 * PF5_ASLOT;
+  const int wm = wave >> 1, wn = wave & 1;  // this wave's 32 x 32 block of the tile
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int tile_m = (int)blockIdx.x / a.tiles_n;
+  const int tile_n = (int)blockIdx.x - tile_m * a.tiles_n;
+  const int m0 = tile_m * PF5_T, n0 = tile_n * PF5_T;
+  const int N = a.N;
+  const int KT = a.K / PF2_BK / KP;  // steps of one part (even: the loop takes two per turn)
+  const int kt0 = kp * KT;
+
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, 0x00020000);
+
+  // activation load i of this wave fills chunk positions [64 (wave XL + i), +64)
+  // of a slot: lane -> row 8 (wave XL + i) + lane / 8, chunk (lane & 7) ^ ((row >> 1) & 7);
+  // rows past M read zeros
+  uint32_t x_off[XL];
+#pragma unroll
+  for (int i = 0; i < XL; ++i) {
+    const int row = 8 * (wave * XL + i) + (lane >> 3);
+    const int c = (lane & 7) ^ ((row >> 1) & 7);
+    const int m = m0 + row;
+    x_off[i] = m < a.M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)c * 16u : OOB;
+  }
+  // packed words: thread -> k8 row wj of the step, columns n0 + wc, n0 + wc + 1
+  const int wj = tid >> 5;
+  const int wc = 2 * (tid & 31);
+  const uint32_t w_off = ((uint32_t)wj * (uint32_t)N + (uint32_t)(n0 + wc)) * 4u;
+  const uint32_t sz_off = (uint32_t)(n0 + wc) * 2u;
+  const uint32_t magic = fp16_magic_vgpr();
+
+  struct Regs {
+    u32x2 w;
+    uint32_t s, z;
+  };
+  // loads of step st of this part (masked past the part: no traffic)
+  auto issue = [&](Regs& r, int st) {
+    const uint32_t mask = st < KT ? 0u : OOB;  // scalar
+    const int t = kt0 + st;
+    __builtin_amdgcn_sched_barrier(0);
+    r.w = __builtin_amdgcn_raw_buffer_load_b64(rq, (w_off + (uint32_t)t * 8u * (uint32_t)N * 4u) | mask, 0, 0);
+    const uint32_t g = (uint32_t)((t * PF2_BK) >> a.gshift);
+    const uint32_t so = (g * (uint32_t)N * 2u + sz_off) | mask;
+    r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
+    r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, so, 0, 0);
+    uint16_t* slot = As + (st % 3) * PF5_ASLOT;
+#pragma unroll
+    for (int i = 0; i < XL; ++i) lds_load16(rx, slot + (wave * XL + i) * 512, (x_off[i] + (uint32_t)t * 128u) | mask);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto dequant = [&](const Regs& r, int b) {
+    uint16_t* buf = Bs + b * PF5_BBUF;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const GroupConst gc = make_group_const((uint16_t)(r.s >> (16 * i)), (uint16_t)(r.z >> (16 * i)));
+      const F f = dequant_word<DT>(r.w[i], gc, magic);
+      const int n = wc + i;
+      *reinterpret_cast<u32x4*>(buf + (n * 8 + (wj ^ ((n >> 1) & 7))) * 8) = __builtin_bit_cast(u32x4, f);
+    }
+  };
+
+  f32x16 acc;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  // fragment offsets (elements) of k sub-step ks inside a 32-row (32-column) block
+  int f_off[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) f_off[ks] = (l32 * 8 + ((2 * ks + lh) ^ ((l32 >> 1) & 7))) * 8;
+  auto multiply = [&](int st) {
+    const uint16_t* A = As + (st % 3) * PF5_ASLOT + wm * 32 * PF2_BK;
+    const uint16_t* B = Bs + (st & 1) * PF5_BBUF + wn * 32 * PF2_BK;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const F af = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(A + f_off[ks]));
+      const F bf = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(B + f_off[ks]));
+      acc = Mfma<DT>::m32(af, bf, acc);
+    }
+  };
+  // this wave's loads of the step have landed and its weight chunks are in
+  // LDS; then every wave's (a raw barrier: a fenced one would wait for the
+  // prefetches too)
+  auto sync_step = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(WAIT_IMM);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // steps in pairs, so that the two register sets alternate statically:
+  // at the barrier of step st, set (st & 1) holds step st + 1's words
+  Regs r0, r1;
+  issue(r0, 0);
+  issue(r1, 1);
+  dequant(r0, 0);
+  for (int st = 0; st < KT; st += 2) {
+    sync_step();
+    issue(r0, st + 2);  // slot (st + 2) % 3 was last read at step st - 1
+    multiply(st);
+    dequant(r1, (st + 1) & 1);  // buffer last read at step st - 1
+    sync_step();
+    issue(r1, st + 3);
+    multiply(st + 1);
+    dequant(r0, st & 1);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // no load (and no LDS write) outstanding past the loop
+  __syncthreads();
+
+  if constexpr (KP > 1) {
+    // parts 1..KP-1 -> LDS (lane-major, conflict-free) -> added to part 0 in part order
+    static_assert((KP - 1) * 4 * 16 * 64 * 4 <= KP * PF5_SET * 2, "partials fit the parts' areas");
+    float* const P = reinterpret_cast<float*>(lds);
+    if (kp > 0) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) P[(((kp - 1) * 4 + wave) * 16 + e) * 64 + lane] = acc[e];
+    }
+    __syncthreads();
+    if (kp == 0) {
+#pragma unroll
+      for (int p = 1; p < KP; ++p)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[e] += P[(((p - 1) * 4 + wave) * 16 + e) * 64 + lane];
+    }
+    __syncthreads();
+  }
+  // output: the tile in LDS (part 0's area), then 16-byte row chunks
+  uint16_t* T = lds;
+  if (kp == 0) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = wm * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
+      T[row * PF5_T + wn * 32 + l32] = float_to_act_bits<DT>(acc[e]);
+    }
+  }
+  __syncthreads();
+  if (a.y16) {
+    for (int c = threadIdx.x; c < PF5_T * PF5_T / 8; c += 256 * KP) {
+      const int row = c >> 3, cc = c & 7;
+      const int m = m0 + row;
+      if (m < a.M)
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&T[row * PF5_T + cc * 8]),
+                                    reinterpret_cast<u32x4*>(a.y + (int64_t)m * a.ldy + n0 + cc * 8));
+    }
+  } else {
+    for (int c = threadIdx.x; c < PF5_T * PF5_T; c += 256 * KP) {
+      const int row = c / PF5_T, col = c - row * PF5_T;
+      const int m = m0 + row;
+      if (m < a.M) a.y[(int64_t)m * a.ldy + n0 + col] = T[c];
+    }
+  }
+}
 }  // namespace w4
 
 using namespace w4host;
@@ -823,6 +1034,32 @@ void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t 
   }
 }
 
+// pf5 (64 x 64 tiles, the weight tile dequantized once per workgroup into
+// LDS) for dense rows where the product has at most one such tile per CU and
+// K <= 4096, with group sizes >= 64 (one group per 64-k step), N % 64 == 0
+// and K a multiple of 128 per K part.  Returns the K parts per workgroup (0:
+// not this kernel).  Four parts except for tall products (M > N), which
+// measured faster with two (k_proj at M = 2048: 13.1 against 14.3 us; q_proj
+// at M = 512 11.7 against 12.4 us, gate_proj at M = 128 11.7 against 12.3
+// us with four).
+int pf5_parts(int64_t M, int64_t N, int64_t K, int64_t G) {
+  if (G < 64 || N % w4::PF5_T != 0 || K > 4096 || K % 128 != 0) return 0;
+  if ((M + w4::PF5_T - 1) / w4::PF5_T * (N / w4::PF5_T) > device_cu_count()) return 0;
+  if (K % 512 == 0 && M <= N) return 4;
+  return K % 256 == 0 ? 2 : 1;
+}
+
+template <int DT>
+void pf5_launch(int parts, const w4::Pf2Args& a, hipStream_t st) {
+  const dim3 grid((unsigned)(((a.M + w4::PF5_T - 1) / w4::PF5_T) * (a.N / w4::PF5_T)));
+  if (parts == 4)
+    hipLaunchKernelGGL((w4::pf5_kernel<DT, 4>), grid, dim3(1024), 0, st, a);
+  else if (parts == 2)
+    hipLaunchKernelGGL((w4::pf5_kernel<DT, 2>), grid, dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL((w4::pf5_kernel<DT, 1>), grid, dim3(256), 0, st, a);
+}
+
 }  // namespace
 
 int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_dtype, void* y, int64_t ldy,
@@ -850,6 +1087,30 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
                       void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st) {
   if (pf2_ok(x, M, N, K, sxm, sxk, qw, sc, ze, y, ldy)) {
+    if (const int parts = pf5_parts(M, N, K, G)) {
+      w4::Pf2Args a{};
+      a.x = static_cast<const uint16_t*>(x);
+      a.qw = reinterpret_cast<const uint32_t*>(qw);
+      a.sc = sc;
+      a.ze = ze;
+      a.y = static_cast<uint16_t*>(y);
+      a.sxm = sxm;
+      a.ldy = ldy;
+      a.x_bytes = (uint32_t)(((M - 1) * sxm + K) * 2);
+      a.qw_bytes = (uint32_t)((K / 8) * N * 4);
+      a.sz_bytes = (uint32_t)((K / G) * N * 2);
+      a.M = (int)M;
+      a.N = (int)N;
+      a.K = (int)K;
+      a.gshift = ilog2(G);
+      a.tiles_n = (int)(N / w4::PF5_T);
+      a.y16 = (ldy % 8 == 0 && (uintptr_t)y % 16 == 0) ? 1 : 0;
+      if (x_dtype == W4_DTYPE_BF16)
+        pf5_launch<W4_DTYPE_BF16>(parts, a, st);
+      else
+        pf5_launch<W4_DTYPE_FP16>(parts, a, st);
+      return check_launch("w4a16_gemm (prefill, pf5)");
+    }
     const Pf2Plan p = plan_pf2(M, N, K);
     if (p.ws > 0 && (ws == nullptr || ws_bytes < p.ws))
       return fail(W4_ERR_WORKSPACE, "w4a16_gemm: workspace of %zu bytes required, %zu given",

@@ -216,6 +216,37 @@ def test_prefill_group_sizes_and_partial_tiles(M, G, NK):
     _check(out, x, qw, s, z, exact_w=_decode(M, G, N, K))
 
 
+# 64 x 64 tiles with the weight tile dequantized once per workgroup into LDS
+# (K in 1 / 2 / 4 parts per workgroup): products with at most one such tile
+# per CU, K <= 4096, group >= 64, N % 64 == 0; ragged M; bit-identical
+# repeats; an output row stride of N + 4 (no 16-byte stores) through the C-ABI,
+# which must leave the padding columns untouched
+@pytest.mark.parametrize("M,N,K,G,dtype", [(2048, 512, 2048, 128, torch.bfloat16),   # two K parts (M > N)
+                                           (512, 2048, 2048, 128, torch.float16),    # four parts
+                                           (128, 8192, 2048, 64, torch.bfloat16),    # four parts, group 64
+                                           (200, 1024, 1024, 256, torch.bfloat16),   # ragged M, group 256
+                                           (130, 2048, 384, 128, torch.float16),     # one part, ragged M
+                                           (320, 640, 768, 64, torch.bfloat16)])     # two parts
+def test_prefill_lds_dequant_tiles(M, N, K, G, dtype):
+    from int4_hip import _lib
+    print(f"[prefill-lds] M={M} N={N} K={K} G={G} {dtype}", flush=True)
+    qw, s, z = _weights(N, K, G, seed=M + N + K)
+    x = randn((M, K), seed=M + 5, dtype=dtype).to(DEV)
+    out = int4_hip.w4a16_matmul(x, qw, s, z)
+    _check(out, x, qw, s, z, exact_w=_decode(M, G, N, K))
+    for _ in range(2):
+        assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
+    lib = _lib.load()
+    xdt = _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_FP16
+    ypad = torch.full((M, N + 4), float("nan"), dtype=dtype, device=DEV)
+    rc = lib.w4a16_gemm(x.data_ptr(), xdt, M, N, K, K, 1, qw.data_ptr(), s.data_ptr(), z.data_ptr(), G,
+                        ypad.data_ptr(), N + 4, None, 0, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "w4a16_gemm")
+    torch.cuda.synchronize()
+    assert torch.equal(ypad[:, :N].view(torch.int16), out.view(torch.int16))
+    assert torch.isnan(ypad[:, N:].float()).all()
+
+
 # shapes whose static plan runs 32-row tiles as workgroups of two K halves
 # (eight waves, the halves summed through LDS)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
