@@ -376,6 +376,125 @@ def summarize_prof(d: Path, kernel: str = ROOFLINE_KERNEL) -> str:
     return "\n".join(out)
 
 
+def summarize_prefill_prof(d: Path) -> str:
+    """Markdown tables of the prefill section (``--only prefill``) from a
+    rocprofv3 run directory laid out as for ``summarize_prof`` (``trace/``,
+    ``fetch/``, ``write/``, ``sq/``).  The section's own dispatches are matched
+    to linears by their order, which every run repeats: per M, the 7-linear
+    block graph (one eager pass and 13 replays), then each linear's graph of 4
+    calls (13 x 4 calls), then the fused 4-call block (14 passes); a call is
+    one main kernel, plus the split-K reduce where the plan splits K.  Times
+    average the last 40 calls of a linear's graph (its 10 timed replays)."""
+    import csv
+
+    def ours(sub, name):
+        f = d / sub / f"run_{name}.csv"
+        if not f.exists():
+            return []
+        # the GEMM kernels only (the weight sets' quantization and the
+        # dequantization for the hipBLASLt comparison are left out)
+        rs = [r for r in csv.DictReader(open(f)) if "w4::" in r["Kernel_Name"] and "quantize" not in r["Kernel_Name"]]
+        return sorted(rs, key=lambda r: int(r["Dispatch_Id"]))
+
+    trace = ours("trace", "kernel_trace")
+    seq = [(r["Kernel_Name"], r["Grid_Size_X"]) for r in trace]
+
+    def counters(sub):
+        # per dispatch (in order of our dispatches): {counter: value}
+        byd = {}
+        for r in ours(sub, "counter_collection"):
+            byd.setdefault(int(r["Dispatch_Id"]), {})[r["Counter_Name"]] = float(r["Counter_Value"])
+        return [byd[k] for k in sorted(byd)]
+
+    fetch, write, sq = counters("fetch"), counters("write"), counters("sq")
+    calib = {}
+    for sub, cname in (("fetch", "FETCH_SIZE"), ("write", "WRITE_SIZE")):
+        f = d / sub / "run_counter_collection.csv"
+        if f.exists():
+            rs = [r for r in csv.DictReader(open(f)) if "copyBuffer" in r["Kernel_Name"] and r["Counter_Name"] == cname]
+            if rs:
+                first = min(int(r["Dispatch_Id"]) for r in rs)
+                calib[cname] = 32768.0 / sum(float(r["Counter_Value"]) for r in rs if int(r["Dispatch_Id"]) == first)
+
+    def period(pos, reps, lo=1):
+        for L in range(lo, (len(seq) - pos) // reps + 1):
+            if seq[pos:pos + reps * L] == seq[pos:pos + L] * reps:
+                return L
+        raise ValueError(f"no repeating dispatch pattern at {pos}")
+
+    def dur(i):
+        return (int(trace[i]["End_Timestamp"]) - int(trace[i]["Start_Timestamp"])) / 1e3
+
+    def avg(idx, f):
+        vals = [f(i) for i in idx]
+        vals = [v for v in vals if v is not None]
+        return sum(vals) / len(vals) if vals else None
+
+    def cval(rows, i, name):
+        return rows[i].get(name) if i < len(rows) else None
+
+    def short(name):
+        return name.replace("void ", "").split("(")[0]
+
+    def wgs(i):
+        return int(trace[i]["Grid_Size_X"]) // max(1, int(trace[i]["Workgroup_Size_X"]))
+
+    lines = ["| M | linear | main kernel | WGs | main us | reduce us | TFLOP/s | traffic MB | alg. MB | "
+             "MFMA busy % | VALU / MFMA instr. | LDS bank conflicts |", "|---|---|---|---|---|---|---|---|---|---|---|---|"]
+    fused = ["| M | call | kernel(s) | WGs | main us | reduce us | MFMA busy % |", "|---|---|---|---|---|---|---|"]
+    pos = 0
+    for M in (128, 512, 2048):
+        pos += 14 * period(pos, 14, 7)  # the 7-linear block graph
+        for name, N, K in LINEARS:
+            L = period(pos, 52)
+            calls = [pos + c * L for c in range(52)][-40:]
+            main = calls
+            red = [c + 1 for c in calls] if L == 2 else []
+            t_main = avg(main, dur)
+            t_red = avg(red, dur) if red else 0.0
+            fs, ws = calib.get("FETCH_SIZE"), calib.get("WRITE_SIZE")
+            traffic = None
+            if fs and ws:
+                f_kib = avg(main, lambda i: cval(fetch, i, "FETCH_SIZE")) or 0.0
+                w_kib = avg(main, lambda i: cval(write, i, "WRITE_SIZE")) or 0.0
+                if red:
+                    f_kib += avg(red, lambda i: cval(fetch, i, "FETCH_SIZE")) or 0.0
+                    w_kib += avg(red, lambda i: cval(write, i, "WRITE_SIZE")) or 0.0
+                traffic = (f_kib * fs + w_kib * ws) * 1024 / 1e6
+            busy = avg(main, lambda i: cval(sq, i, "SQ_VALU_MFMA_BUSY_CYCLES"))
+            valu = avg(main, lambda i: cval(sq, i, "SQ_INSTS_VALU"))
+            mfma = avg(main, lambda i: cval(sq, i, "SQ_INSTS_MFMA"))
+            lds_c = avg(main, lambda i: cval(sq, i, "SQ_LDS_BANK_CONFLICT"))
+            busy_pct = busy / (1024 * t_main * 1e-6 * 2.4e9) * 100 if busy is not None and t_main else None
+            tfl = 2 * M * N * K / ((t_main + t_red) * 1e-6) / 1e12
+            fmt = lambda v, p: "-" if v is None else f"{v:.{p}f}"  # noqa: E731
+            lines.append(f"| {M} | {name.split('_')[0]} | `{short(trace[main[0]]['Kernel_Name'])}` | {wgs(main[0])} | "
+                         f"{t_main:.2f} | {t_red:.2f} | {tfl:.0f} | {fmt(traffic, 1)} | "
+                         f"{lin_bytes(N, K, M) / 1e6:.1f} | {fmt(busy_pct, 1)} | "
+                         f"{fmt(valu / mfma if valu is not None and mfma else None, 2)} | {fmt(lds_c, 0)} |")
+            pos += 52 * L
+        L = period(pos, 14, 4)  # the fused block: q/k/v grouped, o, gate/up grouped, down
+        passes = [pos + p * L for p in range(14)][-10:]
+        pat = seq[pos:pos + L]
+        # calls of the pattern: a reduce kernel belongs to the call before it
+        starts = [i for i in range(L) if "reduce" not in pat[i][0]]
+        for ci, (s0, label) in enumerate(zip(starts, ("q + k + v", "o", "gate + up", "down"))):
+            s1 = starts[ci + 1] if ci + 1 < len(starts) else L
+            main = [p + s0 for p in passes]
+            red = [p + s0 + 1 for p in passes] if s1 - s0 == 2 else []
+            t_main = avg(main, dur)
+            busy = avg(main, lambda i: cval(sq, i, "SQ_VALU_MFMA_BUSY_CYCLES"))
+            busy_pct = busy / (1024 * t_main * 1e-6 * 2.4e9) * 100 if busy is not None and t_main else None
+            fused.append(f"| {M} | {label} | `{short(pat[s0][0])}` | {wgs(main[0])} | {t_main:.2f} | "
+                         f"{avg(red, dur) if red else 0.0:.2f} | {'-' if busy_pct is None else f'{busy_pct:.1f}'} |")
+        pos += 14 * L
+    head = []
+    if calib:
+        head.append(f"- calibration (32 MiB device copy): FETCH_SIZE x {calib.get('FETCH_SIZE', 0):.3f}, "
+                    f"WRITE_SIZE x {calib.get('WRITE_SIZE', 0):.3f}")
+    return "\n".join(head + ["", "Per linear:", ""] + lines + ["", "Fused block (4 calls):", ""] + fused)
+
+
 def profiled_traffic() -> dict | None:
     """HBM bytes per launch of the roofline kernel, from the committed profile."""
     if not PROFILE.exists():
@@ -405,9 +524,14 @@ def main() -> int:
                     help="also run one 32 MiB device copy (for scaling FETCH_SIZE/WRITE_SIZE counters)")
     ap.add_argument("--summarize-prof", default=None, metavar="DIR",
                     help="print the profile summary of a rocprofv3 run directory and exit (no GPU use)")
+    ap.add_argument("--summarize-prefill-prof", default=None, metavar="DIR",
+                    help="print the per-linear tables of a rocprofv3 run of --only prefill and exit (no GPU use)")
     args = ap.parse_args()
     if args.summarize_prof:
         print(summarize_prof(Path(args.summarize_prof)))
+        return 0
+    if args.summarize_prefill_prof:
+        print(summarize_prefill_prof(Path(args.summarize_prefill_prof)))
         return 0
     only = set(args.only.split(",")) if args.only != "all" else {"decode", "perlinear", "splitk", "prefill", "quantize",
                                                                   "llama"}
