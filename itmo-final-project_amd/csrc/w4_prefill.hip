@@ -722,14 +722,21 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 //    reads (32 rows / columns x one chunk per 16 lanes) hit all banks.
 //  * KP sets (KP = 1, 2 or 4 per workgroup, 4 to 16 waves) run the same tile
 //    over KP contiguous parts of K in lockstep, each with its own LDS area
-//    (3 activation slots, 2 weight buffers: 40 KB); the parts are added
+//    (2 activation slots, 2 weight buffers: 32 KB); the parts are added
 //    through LDS in part order at the end, so the result is a fixed function
 //    of the inputs (no atomics, no partial-sum buffer, no reduce launch).
-//  * Loads run two steps ahead: one barrier per step, then the step t + 2
-//    loads are issued, step t is multiplied and the words of step t + 1
-//    (landed a step earlier) are dequantized into the other weight buffer.
-//    Every step issues the same number of loads, so "the activations of step
-//    t have landed" is one fixed s_waitcnt vmcnt before the barrier.
+//  * One barrier per step; after it the activations of step t + 1 and the
+//    packed words of step t + 2 are issued, step t is multiplied and the
+//    words of step t + 1 (loaded a step earlier) are dequantized into the
+//    other weight buffer.  Slots and buffers alternate with the step's
+//    parity, so in the two-step loop body every LDS address is a per-lane
+//    constant plus an immediate, and every load takes its step through the
+//    scalar offset: the only per-step vector instructions are the
+//    dequantization (52 VALU instructions per wave and step, against 74 with
+//    a three-slot ring indexed at run time: 5-10 % faster on the shapes
+//    below).  "The activations of step t + 1 have landed" is then
+//    s_waitcnt vmcnt(3) (only the three word / scale / zero loads issued
+//    after them may be outstanding).
 // Measured against pf3's planned launch (bench shapes, G = 128, bf16):
 // k_proj at M = 2048 17.7 -> 13.1 us (KP = 2), q_proj at M = 512 18.7 ->
 // 11.7 us, k_proj at M = 512 11.5 -> 10.5 us, gate_proj at M = 128 18.9 ->
@@ -740,16 +747,16 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 constexpr int PF5_T = 64;                   // tile rows = tile columns
 constexpr int PF5_ASLOT = PF5_T * PF2_BK;  // elements of one activation slot
 constexpr int PF5_BBUF = PF5_T * PF2_BK;   // elements of one weight buffer
-constexpr int PF5_SET = 3 * PF5_ASLOT + 2 * PF5_BBUF;  // elements of one K part's area (40 KB)
+constexpr int PF5_SET = 2 * PF5_ASLOT + 2 * PF5_BBUF;  // elements of one K part's area (32 KB)
 
 template <int DT, int KP>
 __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   typedef typename Act<DT>::frag F;
   constexpr int XL = PF5_T / 32;  // direct-to-LDS activation loads per thread and step
-  constexpr int NLOAD = 3 + XL;   // loads per thread and step: words, scales, zeros, activations
-  // vmcnt(NLOAD) (only the next step's loads may be outstanding) and lgkmcnt(0)
-  constexpr int WAIT_IMM = (NLOAD & 15) | 0x70 | ((NLOAD >> 4) << 14);
-  static_assert(NLOAD < 16, "vmcnt range");
+  // at the barrier of step t + 1 only the word / scale / zero loads of step
+  // t + 2 (issued after the activations of step t + 1) may be outstanding
+  constexpr int WAIT3 = 3 | 0x70;  // vmcnt(3), lgkmcnt(0)
+  constexpr int WAIT0 = 0 | 0x70;  // vmcnt(0), lgkmcnt(0)
   __shared__ __attribute__((aligned(16))) uint16_t lds[KP * PF5_SET];
   constexpr uint32_t OOB = 0x80000000u;
 
@@ -758,14 +765,14 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   const int tid = threadIdx.x & 255;                                                  // within the part
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   uint16_t* const As = lds + kp * PF5_SET;
-  uint16_t* const Bs = As + 3 * PF5_ASLOT;
+  uint16_t* const Bs = As + 2 * PF5_ASLOT;
   const int wm = wave >> 1, wn = wave & 1;  // this wave's 32 x 32 block of the tile
   const int l32 = lane & 31, lh = lane >> 5;
   const int tile_m = (int)blockIdx.x / a.tiles_n;
   const int tile_n = (int)blockIdx.x - tile_m * a.tiles_n;
   const int m0 = tile_m * PF5_T, n0 = tile_n * PF5_T;
   const int N = a.N;
-  const int KT = a.K / PF2_BK / KP;  // steps of one part (even: the loop takes two per turn)
+  const int KT = a.K / PF2_BK / KP;  // steps of one part (even, >= 2)
   const int kt0 = kp * KT;
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, 0x00020000);
@@ -773,9 +780,8 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rz = __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, 0x00020000);
 
-  // activation load i of this wave fills chunk positions [64 (wave XL + i), +64)
-  // of a slot: lane -> row 8 (wave XL + i) + lane / 8, chunk (lane & 7) ^ ((row >> 1) & 7);
-  // rows past M read zeros
+  // per-lane offsets are loop invariant; the step enters through the scalar
+  // offset of each load (no per-step address arithmetic in the vector ALU)
   uint32_t x_off[XL];
 #pragma unroll
   for (int i = 0; i < XL; ++i) {
@@ -784,31 +790,33 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
     const int m = m0 + row;
     x_off[i] = m < a.M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)c * 16u : OOB;
   }
-  // packed words: thread -> k8 row wj of the step, columns n0 + wc, n0 + wc + 1
   const int wj = tid >> 5;
   const int wc = 2 * (tid & 31);
   const uint32_t w_off = ((uint32_t)wj * (uint32_t)N + (uint32_t)(n0 + wc)) * 4u;
   const uint32_t sz_off = (uint32_t)(n0 + wc) * 2u;
+  // weight chunk (column n, k8 row wj) of a buffer, elements
+  const int b_off0 = (wc * 8 + (wj ^ ((wc >> 1) & 7))) * 8;
+  const int b_off1 = ((wc + 1) * 8 + (wj ^ (((wc + 1) >> 1) & 7))) * 8;
   const uint32_t magic = fp16_magic_vgpr();
 
   struct Regs {
     u32x2 w;
     uint32_t s, z;
   };
-  // loads of step st of this part (masked past the part: no traffic)
-  auto issue = [&](Regs& r, int st) {
-    const uint32_t mask = st < KT ? 0u : OOB;  // scalar
+  auto issue_w = [&](Regs& r, int st) {
     const int t = kt0 + st;
-    __builtin_amdgcn_sched_barrier(0);
-    r.w = __builtin_amdgcn_raw_buffer_load_b64(rq, (w_off + (uint32_t)t * 8u * (uint32_t)N * 4u) | mask, 0, 0);
     const uint32_t g = (uint32_t)((t * PF2_BK) >> a.gshift);
-    const uint32_t so = (g * (uint32_t)N * 2u + sz_off) | mask;
-    r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, so, 0, 0);
-    r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, so, 0, 0);
-    uint16_t* slot = As + (st % 3) * PF5_ASLOT;
+    r.w = __builtin_amdgcn_raw_buffer_load_b64(rq, w_off, (uint32_t)t * 8u * (uint32_t)N * 4u, 0);
+    r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, sz_off, g * (uint32_t)N * 2u, 0);
+    r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, sz_off, g * (uint32_t)N * 2u, 0);
+  };
+  auto issue_a = [&](int st, int slot) {
+    const int t = kt0 + st;
+    uint16_t* base = As + slot * PF5_ASLOT;
 #pragma unroll
-    for (int i = 0; i < XL; ++i) lds_load16(rx, slot + (wave * XL + i) * 512, (x_off[i] + (uint32_t)t * 128u) | mask);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int i = 0; i < XL; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(base + (wave * XL + i) * 512),
+                                               16, x_off[i], (uint32_t)t * 128u, 0, 0);
   };
   auto dequant = [&](const Regs& r, int b) {
     uint16_t* buf = Bs + b * PF5_BBUF;
@@ -816,21 +824,19 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
     for (int i = 0; i < 2; ++i) {
       const GroupConst gc = make_group_const((uint16_t)(r.s >> (16 * i)), (uint16_t)(r.z >> (16 * i)));
       const F f = dequant_word<DT>(r.w[i], gc, magic);
-      const int n = wc + i;
-      *reinterpret_cast<u32x4*>(buf + (n * 8 + (wj ^ ((n >> 1) & 7))) * 8) = __builtin_bit_cast(u32x4, f);
+      *reinterpret_cast<u32x4*>(buf + (i == 0 ? b_off0 : b_off1)) = __builtin_bit_cast(u32x4, f);
     }
   };
 
   f32x16 acc;
 #pragma unroll
   for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
-  // fragment offsets (elements) of k sub-step ks inside a 32-row (32-column) block
   int f_off[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) f_off[ks] = (l32 * 8 + ((2 * ks + lh) ^ ((l32 >> 1) & 7))) * 8;
-  auto multiply = [&](int st) {
-    const uint16_t* A = As + (st % 3) * PF5_ASLOT + wm * 32 * PF2_BK;
-    const uint16_t* B = Bs + (st & 1) * PF5_BBUF + wn * 32 * PF2_BK;
+  auto multiply = [&](int slot) {
+    const uint16_t* A = As + slot * PF5_ASLOT + wm * 32 * PF2_BK;
+    const uint16_t* B = Bs + slot * PF5_BBUF + wn * 32 * PF2_BK;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const F af = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(A + f_off[ks]));
@@ -838,34 +844,55 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
       acc = Mfma<DT>::m32(af, bf, acc);
     }
   };
-  // this wave's loads of the step have landed and its weight chunks are in
-  // LDS; then every wave's (a raw barrier: a fenced one would wait for the
-  // prefetches too)
-  auto sync_step = [&]() {
+  auto sync3 = [&]() {
     __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_waitcnt(WAIT_IMM);
+    __builtin_amdgcn_s_waitcnt(WAIT3);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  auto sync0 = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(WAIT0);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // steps in pairs, so that the two register sets alternate statically:
-  // at the barrier of step st, set (st & 1) holds step st + 1's words
+  // step t: activations of t + 1 and words of t + 2 issued, step t
+  // multiplied (slot and buffer t & 1), words of t + 1 dequantized into
+  // buffer (t + 1) & 1; register set t & 1 receives the words of t + 2
   Regs r0, r1;
-  issue(r0, 0);
-  issue(r1, 1);
+  issue_a(0, 0);
+  issue_w(r0, 0);
+  issue_w(r1, 1);
   dequant(r0, 0);
-  for (int st = 0; st < KT; st += 2) {
-    sync_step();
-    issue(r0, st + 2);  // slot (st + 2) % 3 was last read at step st - 1
-    multiply(st);
-    dequant(r1, (st + 1) & 1);  // buffer last read at step st - 1
-    sync_step();
-    issue(r1, st + 3);
-    multiply(st + 1);
-    dequant(r0, st & 1);
+  int st = 0;
+  for (; st + 2 < KT; st += 2) {
+    sync3();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_a(st + 1, 1);
+    issue_w(r0, st + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(0);
+    dequant(r1, 1);
+    sync3();
+    __builtin_amdgcn_sched_barrier(0);
+    issue_a(st + 2, 0);
+    issue_w(r1, st + 3);
+    __builtin_amdgcn_sched_barrier(0);
+    multiply(1);
+    dequant(r0, 0);
   }
-  __builtin_amdgcn_s_waitcnt(0);  // no load (and no LDS write) outstanding past the loop
+  // the last two steps: no words left to load
+  sync3();
+  issue_a(st + 1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  multiply(0);
+  dequant(r1, 1);
+  sync0();
+  multiply(1);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   if constexpr (KP > 1) {
