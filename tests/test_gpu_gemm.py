@@ -247,6 +247,19 @@ def test_prefill_lds_dequant_tiles(M, N, K, G, dtype):
     assert torch.isnan(ypad[:, N:].float()).all()
 
 
+# the same tiles on activation rows with a stride above K (a column slice of a
+# wider tensor: rows still dense and 16-byte aligned)
+@pytest.mark.parametrize("M,N,K", [(512, 2048, 2048), (2048, 512, 1024)])
+def test_prefill_lds_dequant_tiles_row_stride(M, N, K):
+    print(f"[prefill-lds strided] M={M} N={N} K={K}", flush=True)
+    qw, s, z = _weights(N, K, 128, seed=M + 3 * N + K)
+    x = randn((M, K + 64), seed=M + 9).to(DEV)[:, :K]
+    assert x.stride(0) == K + 64
+    out = int4_hip.w4a16_matmul(x, qw, s, z)
+    _check(out, x, qw, s, z, exact_w=_decode(M, 128, N, K))
+    assert torch.equal(int4_hip.w4a16_matmul(x.contiguous(), qw, s, z).view(torch.int16), out.view(torch.int16))
+
+
 # shapes whose static plan runs 32-row tiles as workgroups of two K halves
 # (eight waves, the halves summed through LDS)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
