@@ -149,9 +149,9 @@ size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, int count, i
  *   1 <= M <= 16: ONE kernel launch for all problems (the factored decode
  *   kernel).  Problems with a long K may be split over several workgroups whose
  *   fp32 partials meet in a fixed order (in `workspace`).
- *   17 <= M <= 64: the same single decode launch, each problem's rows cut into
- *   slices of 16 (group sizes >= 32, 16-byte aligned x), long K split the same
- *   way.
+ *   17 <= M <= 64, and up to M = 128 when every problem has N <= 4096: the
+ *   same single decode launch, each problem's rows cut into slices of 16
+ *   (group sizes >= 32, 16-byte aligned x), long K split the same way.
  *   Otherwise, M > 16: problems that share one activation matrix (same x pointer, K and
  *   group size; at most 4) run as ONE launch of the prefill kernel (no
  *   split-K, the tiles of all problems side by side) when the library's

@@ -41,12 +41,22 @@ static constexpr int64_t kSliceM = 64;
 // too (eight at most): at M = 128 the prefill kernel's plan for these shapes
 // has few tiles and a split-K reduce launch (o_proj 12.5 -> 6.9 us, k_proj
 // 8.9 -> 6.4 us, down_proj 19.2 -> 19.1 us), while for N = 8192 (gate_proj)
-// it was the faster of the two (19.8 against 20.5 us).  Grouped calls above
-// kSliceM keep the shared-activation prefill launch, faster for q/k/v and
-// gate/up together (the 4-call block 69.8 against 79.2 us).
+// it was the faster of the two (19.8 against 20.5 us).  A grouped call above
+// kSliceM takes the slices under the same rule, i.e. when every problem has
+// N <= kSliceLoneN (q/k/v at M = 128: one launch of 384 workgroups; the 4-call
+// block 66.3 -> 59.7 us); with a wider problem (gate/up) it keeps the
+// shared-activation prefill launch, which measured faster there (routing
+// gate/up through the slices too took the 4-call block to 79.2 us).
 static constexpr int64_t kSliceLoneM = 128;
 static constexpr int64_t kSliceLoneN = 4096;
 static bool sliced_lone(int64_t M, int64_t N) { return M <= kSliceM || (M <= kSliceLoneM && N <= kSliceLoneN); }
+static bool sliced_grouped(const w4a16_problem* problems, int count, int64_t M) {
+  if (M <= kSliceM) return true;
+  if (M > kSliceLoneM) return false;
+  for (int i = 0; i < count; ++i)
+    if (problems[i].N > kSliceLoneN) return false;
+  return true;
+}
 
 int w4_decode_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count,
                      int x_dtype, int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes,
@@ -176,7 +186,7 @@ extern "C" size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, i
       const size_t b = w4a16_workspace_bytes(M, problems[i].N, problems[i].K, problems[i].group_size);
       most = b > most ? b : most;
     }
-    if (M <= kSliceM) {
+    if (sliced_grouped(problems, count, M)) {
       int64_t sxm[W4_MAX_GROUPED], mr[W4_MAX_GROUPED];
       for (int i = 0; i < count; ++i) sxm[i] = problems[i].K, mr[i] = M;
       const size_t d = w4_decode_workspace_bytes(problems, sxm, count, kDecodeM, mr);
@@ -207,7 +217,7 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
     // one w4a16_gemm per problem, in order, on the stream (x rows of K
     // elements)
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (M <= kSliceM) {
+    if (sliced_grouped(problems, count, M)) {
       int64_t sxm[W4_MAX_GROUPED], mr[W4_MAX_GROUPED];
       for (int i = 0; i < count; ++i) sxm[i] = problems[i].K, mr[i] = M;
       unsigned* counters;

@@ -159,8 +159,9 @@ def w4a16_matmul_grouped(xs: Sequence[torch.Tensor], weights: Sequence[tuple],
     """Several independent products ``xs[i] @ W_i^T``, fused into one launch.
 
     ``weights[i]`` is a ``(qweight, scales, zeros)`` triple.  All ``xs[i]`` share
-    dtype and the leading size M.  For M <= 64 every problem runs in one decode
-    launch (rows in slices of 16 above M = 16; group sizes >= 32); otherwise
+    dtype and the leading size M.  For M <= 64, and up to M = 128 when every
+    problem has N <= 4096, every problem runs in one decode launch (rows in
+    slices of 16 above M = 16; group sizes >= 32); otherwise
     products of one shared activation tensor (q/k/v, gate/up: pass the same
     tensor) run as one prefill launch when the library's plan allows it, else
     one launch each.  This fuses the per-linear launches

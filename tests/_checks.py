@@ -11,8 +11,9 @@ Tolerances (stated per the task's floating-point bar):
 * the reference's own check against the unrounded fp32 W_hat
   (tests/test_kernels.py:60): rtol 2e-2, atol 2e-2 * max |ref|.
 
-The decode regime (M <= 64, or M <= 128 with N <= 4096 for a lone product;
-group size >= 32, dense activation rows) applies
+The decode regime (M <= 64, or M <= 128 with N <= 4096 for a lone product
+or for every product of a grouped call; group size >= 32, dense activation
+rows) applies
 scales and zero points after the matrix-core sums, so it multiplies by the
 exact fp32 W_hat instead of W_hat rounded to the activation dtype.  Its
 elementwise check is against ref = x @ W_hat_fp32^T with

@@ -110,6 +110,31 @@ def test_grouped_matches_single(M):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
+# grouped products of 65..128 rows whose every N <= 4096 (q/k/v/o shapes): one
+# decode launch of 16-row slices (exact W_hat; the shared-activation prefill
+# launch would round W_hat and miss this bound), repeat calls bit-identical,
+# shared and separate inputs; a wider problem in the group (gate_proj) sends
+# the call back to the prefill kernels
+@pytest.mark.parametrize("M", [65, 96, 128])
+def test_grouped_row_slices_up_to_128(M):
+    print(f"[grouped-slices] M={M}", flush=True)
+    shapes = [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048)]
+    ws = [_weights(N, K, 128, seed=60 + i) for i, (N, K) in enumerate(shapes)]
+    x = randn((M, 2048), seed=70 + M).to(DEV)
+    outs = int4_hip.w4a16_matmul_grouped([x] * len(ws), ws)
+    for (qw, s, z), y in zip(ws, outs):
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+    again = int4_hip.w4a16_matmul_grouped([x] * len(ws), ws)
+    for a, b in zip(outs, again):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    xs = [randn((M, 2048), seed=80 + i).to(DEV) for i in range(len(ws))]
+    for xi, (qw, s, z), y in zip(xs, ws, int4_hip.w4a16_matmul_grouped(xs, ws)):
+        _check(y, xi, qw, s, z, ref_unrounded=False, exact_w=True)
+    wide = ws[:1] + [_weights(8192, 2048, 128, seed=69)]
+    for (qw, s, z), y in zip(wide, int4_hip.w4a16_matmul_grouped([x] * 2, wide)):
+        _check(y, x, qw, s, z, exact_w="either")
+
+
 def test_graph_capture_replays_match_eager():
     qw, s, z = _weights(2048, 2048, 128, seed=5)
     x = randn((16, 2048), seed=6).to(DEV)
