@@ -702,8 +702,8 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 }
 
 // ---------------------------------------------------------------------------
-// pf5_kernel: 64 x 64 output tiles for products with few tiles (at most one
-// per CU), the weight tile dequantized ONCE per workgroup into LDS.
+// pf5_kernel: TS x TS output tiles (TS = 64 or 128) for products with about
+// one tile per CU, the weight tile dequantized ONCE per workgroup into LDS.
 //
 // pf3 gives every wave its own 64 columns and dequantizes them in registers
 // for the wave's rows: cheap per MFMA with 128-row tiles, but a shape such as
@@ -711,9 +711,10 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 // at M = 128 (128 x 8192) has 256 tiles of 64 x 64 at most, so pf3 runs
 // 32-row tiles whose dequantization is repeated for every 32 rows, or split-K
 // with fp32 partials and a reduce launch.  Here:
-//  * A set of four waves computes the 64 x 64 tile as 2 x 2 blocks of
-//    32 x 32 (one v_mfma_f32_32x32x16 accumulator per wave).  Per 64-k step
-//    the set's 256 threads load the 8 x 64 packed words (two adjacent columns
+//  * A set of four waves computes the tile as its 2 x 2 quarters: one
+//    32 x 32 block (one v_mfma_f32_32x32x16 accumulator) per wave for
+//    TS = 64, 2 x 2 such blocks per wave for TS = 128.  Per 64-k step the
+//    set's 256 threads load the 8 x TS packed words (TS / 32 adjacent columns
 //    of one k8 row per thread), dequantize them exactly as pf3 does (fp32
 //    (q - z) * s, one rounding to the activation dtype) and store the bf16 /
 //    fp16 B tile to LDS, column-major with 16-byte chunk (column n, k8 row j)
@@ -722,7 +723,8 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 //    reads (32 rows / columns x one chunk per 16 lanes) hit all banks.
 //  * KP sets (KP = 1, 2 or 4 per workgroup, 4 to 16 waves) run the same tile
 //    over KP contiguous parts of K in lockstep, each with its own LDS area
-//    (2 activation slots, 2 weight buffers: 32 KB); the parts are added
+//    (2 activation slots, 2 weight buffers: 32 KB for TS = 64, 64 KB for
+//    TS = 128, so KP <= 2 there); the parts are added
 //    through LDS in part order at the end, so the result is a fixed function
 //    of the inputs (no atomics, no partial-sum buffer, no reduce launch).
 //  * One barrier per step; after it the activations of step t + 1 and the
@@ -742,35 +744,50 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 // 11.7 us, k_proj at M = 512 11.5 -> 10.5 us, gate_proj at M = 128 18.9 ->
 // 11.7 us (KP = 4); slower where there are more tiles than CUs (q_proj at
 // M = 2048: 33.8 against 25.7 us) or K = 8192 (down_proj at M = 512: 34.8
-// against 33.0 us).  Sub-step software pipelining (pf3's fragment prefetch
-// across the barrier) measured slower here.
-constexpr int PF5_T = 64;                   // tile rows = tile columns
-constexpr int PF5_ASLOT = PF5_T * PF2_BK;  // elements of one activation slot
-constexpr int PF5_BBUF = PF5_T * PF2_BK;   // elements of one weight buffer
-constexpr int PF5_SET = 2 * PF5_ASLOT + 2 * PF5_BBUF;  // elements of one K part's area (32 KB)
+// against 33.0 us).  TS = 128 with two K parts (eight waves, two per SIMD,
+// a 64 x 64 quarter per wave) for products with 0.75 to 1 tile of 128 x 128
+// per CU and K <= 4096, where pf3's plans are 64-row tiles with one wave per
+// SIMD: q_proj at M = 2048 28.5 -> 26.6 us, gate_proj at M = 512 28.2 ->
+// 26.2 us, 2048 x 2048 x 4096 51.3 -> 46.6 us (slower with K = 8192, with
+// more tiles than CUs, or with half the CUs idle).  Sub-step software
+// pipelining (pf3's fragment prefetch across the barrier) measured slower
+// here.
 
-template <int DT, int KP>
+// 16 bytes per lane from a raw buffer straight into LDS at lds + 16 * lane,
+// the buffer offset split into a per-lane and a wave-uniform part.
+__device__ __forceinline__ void lds_load16_so(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset,
+                                              uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0, 0);
+}
+
+template <int DT, int KP, int TS>
 __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   typedef typename Act<DT>::frag F;
-  constexpr int XL = PF5_T / 32;  // direct-to-LDS activation loads per thread and step
+  static_assert(TS == 64 || TS == 128, "tile side");
+  constexpr int WB = TS / 64;     // 32 x 32 blocks per wave side
+  constexpr int XL = TS / 32;     // direct-to-LDS activation loads per thread and step
+  constexpr int WPT = TS / 32;    // packed words per thread and step (adjacent columns)
+  constexpr int ASLOT = TS * PF2_BK;
+  constexpr int BBUF = TS * PF2_BK;
+  constexpr int SET = 4 * TS * PF2_BK;  // one K part: two activation slots, two weight buffers
   // at the barrier of step t + 1 only the word / scale / zero loads of step
   // t + 2 (issued after the activations of step t + 1) may be outstanding
   constexpr int WAIT3 = 3 | 0x70;  // vmcnt(3), lgkmcnt(0)
   constexpr int WAIT0 = 0 | 0x70;  // vmcnt(0), lgkmcnt(0)
-  __shared__ __attribute__((aligned(16))) uint16_t lds[KP * PF5_SET];
+  __shared__ __attribute__((aligned(16))) uint16_t lds[KP * SET];
   constexpr uint32_t OOB = 0x80000000u;
 
   const int lane = threadIdx.x & 63;
   const int kp = KP == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 8);  // K part
   const int tid = threadIdx.x & 255;                                                  // within the part
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  uint16_t* const As = lds + kp * PF5_SET;
-  uint16_t* const Bs = As + 2 * PF5_ASLOT;
-  const int wm = wave >> 1, wn = wave & 1;  // this wave's 32 x 32 block of the tile
+  uint16_t* const As = lds + kp * SET;
+  uint16_t* const Bs = As + 2 * ASLOT;
+  const int wm = wave >> 1, wn = wave & 1;  // this wave's quarter of the tile
   const int l32 = lane & 31, lh = lane >> 5;
   const int tile_m = (int)blockIdx.x / a.tiles_n;
   const int tile_n = (int)blockIdx.x - tile_m * a.tiles_n;
-  const int m0 = tile_m * PF5_T, n0 = tile_n * PF5_T;
+  const int m0 = tile_m * TS, n0 = tile_n * TS;
   const int N = a.N;
   const int KT = a.K / PF2_BK / KP;  // steps of one part (even, >= 2)
   const int kt0 = kp * KT;
@@ -790,58 +807,86 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
     const int m = m0 + row;
     x_off[i] = m < a.M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)c * 16u : OOB;
   }
-  const int wj = tid >> 5;
-  const int wc = 2 * (tid & 31);
+  const int wj = tid >> 5;          // k8 row of this thread's words
+  const int wc = WPT * (tid & 31);  // first of its WPT adjacent columns
   const uint32_t w_off = ((uint32_t)wj * (uint32_t)N + (uint32_t)(n0 + wc)) * 4u;
   const uint32_t sz_off = (uint32_t)(n0 + wc) * 2u;
   // weight chunk (column n, k8 row wj) of a buffer, elements
-  const int b_off0 = (wc * 8 + (wj ^ ((wc >> 1) & 7))) * 8;
-  const int b_off1 = ((wc + 1) * 8 + (wj ^ (((wc + 1) >> 1) & 7))) * 8;
+  int b_off[WPT];
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) b_off[i] = ((wc + i) * 8 + (wj ^ (((wc + i) >> 1) & 7))) * 8;
   const uint32_t magic = fp16_magic_vgpr();
 
   struct Regs {
-    u32x2 w;
-    uint32_t s, z;
+    uint32_t w[WPT];
+    uint32_t s[WPT / 2], z[WPT / 2];
   };
   auto issue_w = [&](Regs& r, int st) {
     const int t = kt0 + st;
     const uint32_t g = (uint32_t)((t * PF2_BK) >> a.gshift);
-    r.w = __builtin_amdgcn_raw_buffer_load_b64(rq, w_off, (uint32_t)t * 8u * (uint32_t)N * 4u, 0);
-    r.s = __builtin_amdgcn_raw_buffer_load_b32(rs, sz_off, g * (uint32_t)N * 2u, 0);
-    r.z = __builtin_amdgcn_raw_buffer_load_b32(rz, sz_off, g * (uint32_t)N * 2u, 0);
+    const uint32_t wso = (uint32_t)t * 8u * (uint32_t)N * 4u, sso = g * (uint32_t)N * 2u;
+    if constexpr (WPT == 4) {
+      const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(rq, w_off, wso, 0);
+      const u32x2 s = __builtin_amdgcn_raw_buffer_load_b64(rs, sz_off, sso, 0);
+      const u32x2 z = __builtin_amdgcn_raw_buffer_load_b64(rz, sz_off, sso, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r.w[i] = w[i];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        r.s[i] = s[i];
+        r.z[i] = z[i];
+      }
+    } else {
+      const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(rq, w_off, wso, 0);
+      r.w[0] = w[0];
+      r.w[1] = w[1];
+      r.s[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, sz_off, sso, 0);
+      r.z[0] = __builtin_amdgcn_raw_buffer_load_b32(rz, sz_off, sso, 0);
+    }
   };
   auto issue_a = [&](int st, int slot) {
     const int t = kt0 + st;
-    uint16_t* base = As + slot * PF5_ASLOT;
+    uint16_t* base = As + slot * ASLOT;
 #pragma unroll
     for (int i = 0; i < XL; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (__attribute__((address_space(3))) void*)(base + (wave * XL + i) * 512),
-                                               16, x_off[i], (uint32_t)t * 128u, 0, 0);
+      lds_load16_so(rx, base + (wave * XL + i) * 512, x_off[i], (uint32_t)t * 128u);
   };
   auto dequant = [&](const Regs& r, int b) {
-    uint16_t* buf = Bs + b * PF5_BBUF;
+    uint16_t* buf = Bs + b * BBUF;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const GroupConst gc = make_group_const((uint16_t)(r.s >> (16 * i)), (uint16_t)(r.z >> (16 * i)));
+    for (int i = 0; i < WPT; ++i) {
+      const GroupConst gc = make_group_const((uint16_t)(r.s[i >> 1] >> (16 * (i & 1))), (uint16_t)(r.z[i >> 1] >> (16 * (i & 1))));
       const F f = dequant_word<DT>(r.w[i], gc, magic);
-      *reinterpret_cast<u32x4*>(buf + (i == 0 ? b_off0 : b_off1)) = __builtin_bit_cast(u32x4, f);
+      *reinterpret_cast<u32x4*>(buf + b_off[i]) = __builtin_bit_cast(u32x4, f);
     }
   };
 
-  f32x16 acc;
+  f32x16 acc[WB][WB];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+  for (int i = 0; i < WB; ++i)
+#pragma unroll
+    for (int j = 0; j < WB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
   int f_off[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) f_off[ks] = (l32 * 8 + ((2 * ks + lh) ^ ((l32 >> 1) & 7))) * 8;
+  // blocks 32 rows / columns apart have the same swizzle: an immediate offset
   auto multiply = [&](int slot) {
-    const uint16_t* A = As + slot * PF5_ASLOT + wm * 32 * PF2_BK;
-    const uint16_t* B = Bs + slot * PF5_BBUF + wn * 32 * PF2_BK;
+    const uint16_t* A = As + slot * ASLOT + wm * (TS / 2) * PF2_BK;
+    const uint16_t* B = Bs + slot * BBUF + wn * (TS / 2) * PF2_BK;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const F af = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(A + f_off[ks]));
-      const F bf = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(B + f_off[ks]));
-      acc = Mfma<DT>::m32(af, bf, acc);
+      F af[WB], bf[WB];
+#pragma unroll
+      for (int i = 0; i < WB; ++i) {
+        af[i] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(A + i * 32 * PF2_BK + f_off[ks]));
+        bf[i] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(B + i * 32 * PF2_BK + f_off[ks]));
+      }
+#pragma unroll
+      for (int i = 0; i < WB; ++i)
+#pragma unroll
+        for (int j = 0; j < WB; ++j) acc[i][j] = Mfma<DT>::m32(af[i], bf[j], acc[i][j]);
     }
   };
   auto sync3 = [&]() {
@@ -895,44 +940,63 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
+  constexpr int PER = WB * WB * 16;  // accumulator floats per lane
   if constexpr (KP > 1) {
-    // parts 1..KP-1 -> LDS (lane-major, conflict-free) -> added to part 0 in part order
-    static_assert((KP - 1) * 4 * 16 * 64 * 4 <= KP * PF5_SET * 2, "partials fit the parts' areas");
-    float* const P = reinterpret_cast<float*>(lds);
+    // parts 1..KP-1 -> LDS (lane-major, conflict-free) -> added to part 0 in part
+    // order.  Part p's wave w writes its accumulators at P + (p * 4 + w) * PER *
+    // 64, element e of the lane at e * 64 + lane (slot 0 unused: every store
+    // offset is a non-negative immediate, so the stores pair up)
+    static_assert(KP * 4 * PER * 64 * 4 <= KP * SET * 2, "partials fit the parts' areas");
+    float* const P = reinterpret_cast<float*>(lds) + wave * PER * 64 + lane;
     if (kp > 0) {
+      float* const Pw = P + kp * 4 * PER * 64;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) P[(((kp - 1) * 4 + wave) * 16 + e) * 64 + lane] = acc[e];
+      for (int i = 0; i < WB; ++i)
+#pragma unroll
+        for (int j = 0; j < WB; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) Pw[((i * WB + j) * 16 + e) * 64] = acc[i][j][e];
     }
     __syncthreads();
     if (kp == 0) {
 #pragma unroll
       for (int p = 1; p < KP; ++p)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) acc[e] += P[(((p - 1) * 4 + wave) * 16 + e) * 64 + lane];
+        for (int i = 0; i < WB; ++i)
+#pragma unroll
+          for (int j = 0; j < WB; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] += P[(p * 4 * PER + (i * WB + j) * 16 + e) * 64];
     }
     __syncthreads();
   }
   // output: the tile in LDS (part 0's area), then 16-byte row chunks
+  static_assert(TS * TS <= SET, "output tile fits part 0's area");
   uint16_t* T = lds;
   if (kp == 0) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int row = wm * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
-      T[row * PF5_T + wn * 32 + l32] = float_to_act_bits<DT>(acc[e]);
-    }
+    for (int i = 0; i < WB; ++i)
+#pragma unroll
+      for (int j = 0; j < WB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = wm * (TS / 2) + i * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
+          T[row * TS + wn * (TS / 2) + j * 32 + l32] = float_to_act_bits<DT>(acc[i][j][e]);
+        }
   }
   __syncthreads();
+  constexpr int CPR = TS / 8;  // 16-byte chunks per tile row
   if (a.y16) {
-    for (int c = threadIdx.x; c < PF5_T * PF5_T / 8; c += 256 * KP) {
-      const int row = c >> 3, cc = c & 7;
+    for (int c = threadIdx.x; c < TS * CPR; c += 256 * KP) {
+      const int row = c / CPR, cc = c - row * CPR;
       const int m = m0 + row;
       if (m < a.M)
-        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&T[row * PF5_T + cc * 8]),
+        __builtin_nontemporal_store(*reinterpret_cast<const u32x4*>(&T[row * TS + cc * 8]),
                                     reinterpret_cast<u32x4*>(a.y + (int64_t)m * a.ldy + n0 + cc * 8));
     }
   } else {
-    for (int c = threadIdx.x; c < PF5_T * PF5_T; c += 256 * KP) {
-      const int row = c / PF5_T, col = c - row * PF5_T;
+    for (int c = threadIdx.x; c < TS * TS; c += 256 * KP) {
+      const int row = c / TS, col = c - row * TS;
       const int m = m0 + row;
       if (m < a.M) a.y[(int64_t)m * a.ldy + n0 + col] = T[c];
     }
@@ -1061,30 +1125,47 @@ void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t 
   }
 }
 
-// pf5 (64 x 64 tiles, the weight tile dequantized once per workgroup into
-// LDS) for dense rows where the product has at most one such tile per CU and
-// K <= 4096, with group sizes >= 64 (one group per 64-k step), N % 64 == 0
-// and K a multiple of 128 per K part.  Returns the K parts per workgroup (0:
-// not this kernel).  Four parts except for tall products (M > N), which
-// measured faster with two (k_proj at M = 2048: 13.1 against 14.3 us; q_proj
-// at M = 512 11.7 against 12.4 us, gate_proj at M = 128 11.7 against 12.3
-// us with four).
-int pf5_parts(int64_t M, int64_t N, int64_t K, int64_t G) {
-  if (G < 64 || N % w4::PF5_T != 0 || K > 4096 || K % 128 != 0) return 0;
-  if ((M + w4::PF5_T - 1) / w4::PF5_T * (N / w4::PF5_T) > device_cu_count()) return 0;
-  if (K % 512 == 0 && M <= N) return 4;
-  return K % 256 == 0 ? 2 : 1;
+// pf5 (TS x TS tiles, the weight tile dequantized once per workgroup into
+// LDS) for dense rows with group sizes >= 64 (one group per 64-k step) and
+// K <= 4096, a multiple of 128 per K part.  parts = K parts per workgroup
+// (0: not this kernel).
+//  * TS = 64 where the product has at most one 64 x 64 tile per CU (N % 64
+//    == 0): four parts except for tall products (M > N), which measured
+//    faster with two (k_proj at M = 2048: 13.1 against 14.3 us; q_proj at
+//    M = 512 11.7 against 12.4 us, gate_proj at M = 128 11.7 against 12.3 us
+//    with four).
+//  * TS = 128 with two parts where it has 0.75 to 1 tile of 128 x 128 per CU
+//    (N % 128 == 0, K % 256 == 0).
+struct Pf5Plan {
+  int parts = 0, ts = 64;
+};
+Pf5Plan pf5_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
+  Pf5Plan p;
+  if (G < 64 || K > 4096 || K % 128 != 0) return p;
+  const int64_t cus = device_cu_count();
+  if (N % 64 == 0 && (M + 63) / 64 * (N / 64) <= cus) {
+    p.parts = (K % 512 == 0 && M <= N) ? 4 : K % 256 == 0 ? 2 : 1;
+    return p;
+  }
+  const int64_t t128 = (M + 127) / 128 * (N / 128);
+  if (N % 128 == 0 && K % 256 == 0 && 4 * t128 >= 3 * cus && t128 <= cus) {
+    p.parts = 2;
+    p.ts = 128;
+  }
+  return p;
 }
 
 template <int DT>
-void pf5_launch(int parts, const w4::Pf2Args& a, hipStream_t st) {
-  const dim3 grid((unsigned)(((a.M + w4::PF5_T - 1) / w4::PF5_T) * (a.N / w4::PF5_T)));
-  if (parts == 4)
-    hipLaunchKernelGGL((w4::pf5_kernel<DT, 4>), grid, dim3(1024), 0, st, a);
-  else if (parts == 2)
-    hipLaunchKernelGGL((w4::pf5_kernel<DT, 2>), grid, dim3(512), 0, st, a);
+void pf5_launch(const Pf5Plan& p, const w4::Pf2Args& a, hipStream_t st) {
+  const dim3 grid((unsigned)(((a.M + p.ts - 1) / p.ts) * (a.N / p.ts)));
+  if (p.ts == 128)
+    hipLaunchKernelGGL((w4::pf5_kernel<DT, 2, 128>), grid, dim3(512), 0, st, a);
+  else if (p.parts == 4)
+    hipLaunchKernelGGL((w4::pf5_kernel<DT, 4, 64>), grid, dim3(1024), 0, st, a);
+  else if (p.parts == 2)
+    hipLaunchKernelGGL((w4::pf5_kernel<DT, 2, 64>), grid, dim3(512), 0, st, a);
   else
-    hipLaunchKernelGGL((w4::pf5_kernel<DT, 1>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((w4::pf5_kernel<DT, 1, 64>), grid, dim3(256), 0, st, a);
 }
 
 }  // namespace
@@ -1114,7 +1195,7 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
                       void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st) {
   if (pf2_ok(x, M, N, K, sxm, sxk, qw, sc, ze, y, ldy)) {
-    if (const int parts = pf5_parts(M, N, K, G)) {
+    if (const Pf5Plan p5 = pf5_plan(M, N, K, G); p5.parts) {
       w4::Pf2Args a{};
       a.x = static_cast<const uint16_t*>(x);
       a.qw = reinterpret_cast<const uint32_t*>(qw);
@@ -1130,12 +1211,12 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
       a.N = (int)N;
       a.K = (int)K;
       a.gshift = ilog2(G);
-      a.tiles_n = (int)(N / w4::PF5_T);
+      a.tiles_n = (int)(N / p5.ts);
       a.y16 = (ldy % 8 == 0 && (uintptr_t)y % 16 == 0) ? 1 : 0;
       if (x_dtype == W4_DTYPE_BF16)
-        pf5_launch<W4_DTYPE_BF16>(parts, a, st);
+        pf5_launch<W4_DTYPE_BF16>(p5, a, st);
       else
-        pf5_launch<W4_DTYPE_FP16>(parts, a, st);
+        pf5_launch<W4_DTYPE_FP16>(p5, a, st);
       return check_launch("w4a16_gemm (prefill, pf5)");
     }
     const Pf2Plan p = plan_pf2(M, N, K);

@@ -241,17 +241,23 @@ def test_prefill_group_sizes_and_partial_tiles(M, G, NK):
     _check(out, x, qw, s, z, exact_w=_decode(M, G, N, K))
 
 
-# 64 x 64 tiles with the weight tile dequantized once per workgroup into LDS
-# (K in 1 / 2 / 4 parts per workgroup): products with at most one such tile
-# per CU, K <= 4096, group >= 64, N % 64 == 0; ragged M; bit-identical
-# repeats; an output row stride of N + 4 (no 16-byte stores) through the C-ABI,
-# which must leave the padding columns untouched
+# tiles whose weight tile is dequantized once per workgroup into LDS: 64 x 64
+# (K in 1 / 2 / 4 parts per workgroup) for products with at most one such
+# tile per CU, and 128 x 128 (two K parts, a 64 x 64 quarter per wave) for
+# products with 0.75 to 1 such tile per CU (256 CUs: 192..256 tiles); K <=
+# 4096, group >= 64; ragged M; bit-identical repeats; an output row stride of
+# N + 4 (no 16-byte stores) through the C-ABI, which must leave the padding
+# columns untouched
 @pytest.mark.parametrize("M,N,K,G,dtype", [(2048, 512, 2048, 128, torch.bfloat16),   # two K parts (M > N)
                                            (512, 2048, 2048, 128, torch.float16),    # four parts
                                            (128, 8192, 2048, 64, torch.bfloat16),    # four parts, group 64
                                            (200, 1024, 1024, 256, torch.bfloat16),   # ragged M, group 256
                                            (130, 2048, 384, 128, torch.float16),     # one part, ragged M
-                                           (320, 640, 768, 64, torch.bfloat16)])     # two parts
+                                           (320, 640, 768, 64, torch.bfloat16),      # two parts
+                                           (2048, 2048, 2048, 128, torch.bfloat16),  # 128 x 128, 256 tiles
+                                           (512, 8192, 2048, 256, torch.float16),    # 128 x 128, group 256
+                                           (1536, 2048, 1024, 64, torch.float16),    # 128 x 128, 192 tiles, group 64
+                                           (1900, 2048, 768, 128, torch.bfloat16)])  # 128 x 128, ragged M
 def test_prefill_lds_dequant_tiles(M, N, K, G, dtype):
     from int4_hip import _lib
     print(f"[prefill-lds] M={M} N={N} K={K} G={G} {dtype}", flush=True)
@@ -274,7 +280,7 @@ def test_prefill_lds_dequant_tiles(M, N, K, G, dtype):
 
 # the same tiles on activation rows with a stride above K (a column slice of a
 # wider tensor: rows still dense and 16-byte aligned)
-@pytest.mark.parametrize("M,N,K", [(512, 2048, 2048), (2048, 512, 1024)])
+@pytest.mark.parametrize("M,N,K", [(512, 2048, 2048), (2048, 512, 1024), (2048, 2048, 2048)])
 def test_prefill_lds_dequant_tiles_row_stride(M, N, K):
     print(f"[prefill-lds strided] M={M} N={N} K={K}", flush=True)
     qw, s, z = _weights(N, K, 128, seed=M + 3 * N + K)
