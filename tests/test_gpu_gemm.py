@@ -464,3 +464,84 @@ def test_decode_rows_ksplit(M, N, K, G):
         _poison_workspace()
         again = int4_hip.w4a16_matmul(x, qw, s, z)
         assert torch.equal(again.view(torch.int16), first.view(torch.int16))
+
+
+def _random_cases(n=30, seed=2024, cap=1.5e9):
+    """Seeded shapes over every routing regime: M = 1, 2..16, 17..64,
+    65..128 and above; N odd or even, multiples of 128 half the time (the
+    tiled fast paths); group sizes 32..256; K up to 8192; bf16 / fp16; a
+    quarter of them on strided activations (x[:, ::2], the split-K paths)."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        lo, hi = [(1, 1), (2, 16), (17, 64), (65, 128), (129, 2600)][i % 5]
+        M = int(rng.integers(lo, hi + 1))
+        G = int(rng.choice([32, 64, 128, 256]))
+        K = G * int(rng.integers(1, max(2, 8192 // G) + 1))
+        N = 128 * int(rng.integers(1, 65)) if rng.random() < 0.5 else int(rng.integers(1, 4097))
+        while M * N * K > cap and (K > G or N > 1):  # K first: keep the tiled widths
+            if K > G:
+                K = max(G, K // 2 // G * G)
+            else:
+                N = max(1, N // 2)
+        out.append((M, N, K, G, bool(rng.random() < 0.25), bool(rng.random() < 0.5)))
+    return out
+
+
+# every routing regime on seeded random shapes against the oracle (exact W_hat
+# where the factored decode kernel takes the product, rounded W_hat elsewhere),
+# repeat calls bit-identical
+@pytest.mark.parametrize("M,N,K,G,strided,fp16", _random_cases())
+def test_random_shapes_against_oracle(M, N, K, G, strided, fp16):
+    dtype = torch.float16 if fp16 else torch.bfloat16
+    print(f"[random] M={M} N={N} K={K} G={G} strided={strided} {dtype}", flush=True)
+    qw, s, z = _weights(N, K, G, seed=M + 3 * N + 7 * K + G)
+    if strided:
+        x = randn((M, 2 * K), seed=M + K, dtype=dtype).to(DEV)[:, ::2]
+    else:
+        x = randn((M, K), seed=M + K, dtype=dtype).to(DEV)
+    out = int4_hip.w4a16_matmul(x, qw, s, z)
+    assert out.shape == (M, N) and out.dtype == dtype
+    _check(out, x, qw, s, z, exact_w=(not strided) and _decode(M, G, N, K))
+    assert torch.equal(int4_hip.w4a16_matmul(x, qw, s, z).view(torch.int16), out.view(torch.int16))
+
+
+def _random_grouped_cases(n=12, seed=77):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        lo, hi = [(1, 1), (2, 16), (17, 64), (65, 128), (129, 700)][i % 5]
+        M = int(rng.integers(lo, hi + 1))
+        G = int(rng.choice([32, 64, 128]))
+        K = G * int(rng.integers(1, 4096 // G + 1))
+        count = int(rng.integers(1, 5))
+        Ns = tuple(128 * int(rng.integers(1, 49)) if rng.random() < 0.6 else int(rng.integers(1, 3000))
+                   for _ in range(count))
+        out.append((M, K, G, Ns, bool(rng.random() < 0.5)))
+    return out
+
+
+# grouped products on seeded random shapes: one shared activation or one per
+# problem, every output against the oracle (exact W_hat where the grouped call
+# must take the decode launch, rounded where it must take the prefill kernels,
+# either bound where a per-problem fallback may take either), repeats
+# bit-identical
+@pytest.mark.parametrize("M,K,G,Ns,shared", _random_grouped_cases())
+def test_random_grouped_against_oracle(M, K, G, Ns, shared):
+    print(f"[random grouped] M={M} K={K} G={G} Ns={Ns} shared={shared}", flush=True)
+    ws = [_weights(N, K, G, seed=500 + 11 * i + N) for i, N in enumerate(Ns)]
+    if shared:
+        xs = [randn((M, K), seed=600 + M).to(DEV)] * len(Ns)
+    else:
+        xs = [randn((M, K), seed=610 + M + i).to(DEV) for i in range(len(Ns))]
+    if M <= 64 or (M <= 128 and all(N <= 4096 for N in Ns)):
+        ew = True        # one decode launch (group sizes >= 32)
+    elif M > 128:
+        ew = False       # prefill kernels (shared or one call per problem)
+    else:
+        ew = "either"    # 65..128 rows with a wide problem: per-problem routes
+    outs = int4_hip.w4a16_matmul_grouped(xs, ws)
+    for x, (qw, s, z), y in zip(xs, ws, outs):
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=ew)
+    for a, b in zip(outs, int4_hip.w4a16_matmul_grouped(xs, ws)):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
