@@ -1,7 +1,17 @@
 // Prefill W4A16 GEMM (M > 64) for gfx950: y[M, N] = x[M, K] @ W_hat^T.
 //
-// Tiling (this library's own design; the reference's Triton kernel is
-// int4_triton/gemm.py:74-157 with the M > 64 launch at :270-296):
+// Kernels in this file (this library's own design; the reference's Triton
+// kernel is int4_triton/gemm.py:74-157 with the M > 64 launch at :270-296):
+//  * pf3_kernel: the main path (dense 16-byte aligned rows, K % 64 == 0);
+//    128 / 64 / 32-row tiles of 64 columns per wave, activations through an
+//    LDS ring, each wave's packed words dequantized in registers, cost-model
+//    split-K (below).
+//  * pf5_kernel: products with about one tile per CU; the weight tile is
+//    dequantized once per workgroup into LDS (below).
+//  * pf2_kernel: pf3's tiling for K % 64 != 0.
+//  * prefill_kernel: strided or unaligned activations, described next.
+//
+// prefill_kernel:
 //  * Workgroup tile BM x BN = 128 x 256, K step BK = 64, four waves side by
 //    side along N, each owning a 128 x 64 output block computed with
 //    v_mfma_f32_32x32x16_{bf16,f16} (4 x 2 blocks of 32 x 32, fp32 accumulate).
