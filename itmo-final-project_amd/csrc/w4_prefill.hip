@@ -414,9 +414,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 //    means every wave is done with step t - 1, whose LDS slot ((t + 3) % 4)
 //    and register set ((t + 3) % 3, last dequantized during sub-step 2) are
 //    then refilled for step t + 3.
-// 16 bytes per lane from a raw buffer straight into LDS at lds + 16 * lane.
-__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
+// 16 bytes per lane from a raw buffer straight into LDS at lds + 16 * lane,
+// the buffer offset split into a per-lane and a wave-uniform part.
+__device__ __forceinline__ void lds_load16_so(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset,
+                                              uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0, 0);
 }
 
 // KH = 2: the workgroup holds two sets of NW waves that run the same tile
@@ -497,25 +499,34 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
     u32x2 w[4];
     uint32_t s[NSZ], z[NSZ];
   };
+  // The step enters every load through the scalar offset (the per-lane offsets
+  // are loop invariant: no per-step vector address arithmetic).  Prefetches
+  // past this split's last step, which no step consumes, reload that last
+  // step, so every load stays inside its tensor.
   auto issue = [&](Regs& r, int st) {  // step st (0-based within this split)
-    const uint32_t lmask = st < nsteps ? 0u : OOB;  // scalar
-    const int kt = kt0 + st;
+    const int kt = kt0 + (st < nsteps ? st : nsteps - 1);  // scalar
     uint16_t* slot = xs + (st & 3) * SLOT;
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < XL; ++j)
-      lds_load16(rx, slot + (wn * XL + j) * 512, (x_off[j] + (uint32_t)kt * PF2_BK * 2u) | lmask);
+      lds_load16_so(rx, slot + (wn * XL + j) * 512, x_off[j], (uint32_t)kt * PF2_BK * 2u);
 #pragma unroll
     for (int j = 0; j < NSZ; ++j) {
-      const uint32_t g = (uint32_t)((kt * PF2_BK + (SZK ? j * 16 + lh * 8 : 0)) >> a.gshift);
-      const uint32_t off = (g * (uint32_t)N * 2u + sz_col) | lmask;
-      r.s[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
-      r.z[j] = __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0);
+      if constexpr (SZK) {  // groups below 64: the group depends on the lane's k half
+        const uint32_t g = (uint32_t)((kt * PF2_BK + j * 16 + lh * 8) >> a.gshift);
+        const uint32_t off = g * (uint32_t)N * 2u + sz_col;
+        r.s[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0);
+        r.z[j] = __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0);
+      } else {
+        const uint32_t g = (uint32_t)((kt * PF2_BK) >> a.gshift);
+        r.s[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, sz_col, g * (uint32_t)N * 2u, 0);
+        r.z[j] = __builtin_amdgcn_raw_buffer_load_b32(rz, sz_col, g * (uint32_t)N * 2u, 0);
+      }
     }
-    const uint32_t wo = ((uint32_t)kt * 8u * (uint32_t)N * 4u + w_lane) | lmask;
+    const uint32_t wso = (uint32_t)kt * 8u * (uint32_t)N * 4u;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      r.w[ks] = __builtin_amdgcn_raw_buffer_load_b64(rq, wo + (uint32_t)ks * 2u * (uint32_t)N * 4u, 0, 0);
+      r.w[ks] = __builtin_amdgcn_raw_buffer_load_b64(rq, w_lane, wso + (uint32_t)ks * 2u * (uint32_t)N * 4u, 0);
     __builtin_amdgcn_sched_barrier(0);
   };
 
@@ -763,12 +774,6 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 // pipelining (pf3's fragment prefetch across the barrier) measured slower
 // here.
 
-// 16 bytes per lane from a raw buffer straight into LDS at lds + 16 * lane,
-// the buffer offset split into a per-lane and a wave-uniform part.
-__device__ __forceinline__ void lds_load16_so(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset,
-                                              uint32_t soffset) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, soffset, 0, 0);
-}
 
 template <int DT, int KP, int TS>
 __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
