@@ -111,25 +111,43 @@ static void split_workspace(void* ws, size_t ws_bytes, unsigned** counters, void
   *scratch_bytes = ws_bytes - W4_WORKSPACE_COUNTER_BYTES;
 }
 
+// Argument checks of w4a16_gemm (and w4a16_gemm_noalloc, which runs them
+// before it enqueues anything).  Sets *empty for a valid call with nothing to
+// compute (M == 0 or N == 0).
+static int gemm_validate(const char* who, const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
+                         const int32_t* qweight, const uint16_t* scales, const uint16_t* zeros, int group_size,
+                         const void* y, int64_t ldy, bool* empty) {
+  *empty = false;
+  if (x_dtype != W4_DTYPE_BF16 && x_dtype != W4_DTYPE_FP16)
+    return fail(W4_ERR_INVALID, "%s: x dtype must be bf16 or fp16 (got code %d)", who, x_dtype);
+  if (M < 0 || N < 0 || K < 8 || K % 8 != 0)
+    return fail(W4_ERR_INVALID, "%s: bad shape M=%lld N=%lld K=%lld", who, (long long)M, (long long)N,
+                (long long)K);
+  const int64_t G = group_size;
+  if (G < 8 || !is_pow2(G) || K % G != 0)
+    return fail(W4_ERR_INVALID, "%s: group_size %d must be a power of two >= 8 dividing K=%lld", who,
+                group_size, (long long)K);
+  if (ldy < N) return fail(W4_ERR_INVALID, "%s: ldy (%lld) < N (%lld)", who, (long long)ldy, (long long)N);
+  if (M == 0 || N == 0) {
+    *empty = true;
+    return W4_OK;
+  }
+  if (!x || !qweight || !scales || !zeros || !y) return fail(W4_ERR_INVALID, "%s: null pointer", who);
+  if (((uintptr_t)x % 2) != 0 || ((uintptr_t)y % 2) != 0)
+    return fail(W4_ERR_INVALID, "%s: x and y must be 2-byte aligned", who);
+  return W4_OK;
+}
+
 extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K,
                           int64_t stride_xm, int64_t stride_xk, const int32_t* qweight,
                           const uint16_t* scales, const uint16_t* zeros, int group_size, void* y,
                           int64_t ldy, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
-  if (x_dtype != W4_DTYPE_BF16 && x_dtype != W4_DTYPE_FP16)
-    return fail(W4_ERR_INVALID, "w4a16_gemm: x dtype must be bf16 or fp16 (got code %d)", x_dtype);
-  if (M < 0 || N < 0 || K < 8 || K % 8 != 0)
-    return fail(W4_ERR_INVALID, "w4a16_gemm: bad shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
-                (long long)K);
+  bool empty;
+  const int vrc = gemm_validate("w4a16_gemm", x, x_dtype, M, N, K, qweight, scales, zeros, group_size, y, ldy,
+                                &empty);
+  if (vrc != W4_OK || empty) return vrc;
   const int64_t G = group_size;
-  if (G < 8 || !is_pow2(G) || K % G != 0)
-    return fail(W4_ERR_INVALID, "w4a16_gemm: group_size %d must be a power of two >= 8 dividing K=%lld",
-                group_size, (long long)K);
-  if (ldy < N) return fail(W4_ERR_INVALID, "w4a16_gemm: ldy (%lld) < N (%lld)", (long long)ldy, (long long)N);
-  if (M == 0 || N == 0) return W4_OK;
-  if (!x || !qweight || !scales || !zeros || !y) return fail(W4_ERR_INVALID, "w4a16_gemm: null pointer");
-  if (((uintptr_t)x % 2) != 0 || ((uintptr_t)y % 2) != 0)
-    return fail(W4_ERR_INVALID, "w4a16_gemm: x and y must be 2-byte aligned");
   hipStream_t st = static_cast<hipStream_t>(stream);
   unsigned* counters;
   void* scratch;
@@ -301,13 +319,12 @@ extern "C" int w4a16_gemm_noalloc(const void* x, int x_dtype, int64_t M, int64_t
                                   const uint16_t* scales, const uint16_t* zeros, int group_size, void* y,
                                   int64_t ldy, void* stream) {
   clear_error();
-  // the same validation as w4a16_gemm, before the scratch size is asked for
-  if (x_dtype != W4_DTYPE_BF16 && x_dtype != W4_DTYPE_FP16)
-    return fail(W4_ERR_INVALID, "w4a16_gemm_noalloc: x dtype must be bf16 or fp16 (got code %d)", x_dtype);
-  if (M < 0 || N < 0 || K < 8 || K % 8 != 0 || group_size < 8 || !is_pow2(group_size) || K % group_size != 0)
-    return fail(W4_ERR_INVALID, "w4a16_gemm_noalloc: bad shape M=%lld N=%lld K=%lld group_size=%d",
-                (long long)M, (long long)N, (long long)K, group_size);
-  if (M == 0 || N == 0) return W4_OK;
+  // every check of w4a16_gemm, before the scratch size is asked for and before
+  // anything is enqueued: a rejected call leaves nothing on the stream
+  bool empty;
+  const int vrc = gemm_validate("w4a16_gemm_noalloc", x, x_dtype, M, N, K, qweight, scales, zeros, group_size, y,
+                                ldy, &empty);
+  if (vrc != W4_OK || empty) return vrc;
   const size_t need = w4a16_workspace_bytes(M, N, K, group_size);
   if (need > (size_t)W4_NOALLOC_SCRATCH_BYTES)
     return fail(W4_ERR_WORKSPACE,

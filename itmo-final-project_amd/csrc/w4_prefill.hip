@@ -482,8 +482,16 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
     const int m = m0 + row;
     x_off[j] = m < a.M ? (uint32_t)((int64_t)m * a.sxm * 2) + (uint32_t)c * 16u : OOB;
   }
-  const uint32_t w_lane = ((uint32_t)lh * (uint32_t)N + (uint32_t)(n0w + 2 * l32)) * 4u;
-  const uint32_t sz_col = (uint32_t)(n0w + 2 * l32) * 2u;
+  // The buffer range check covers the per-lane (VGPR) offset plus the
+  // immediate, not the scalar offset that carries the step: a lane whose two
+  // columns lie past N (a partial last tile; N is even, so a lane's pair is
+  // either inside or past the end) would read past the end of qweight (or of
+  // scales / zeros) on the last k8 rows.  Those lanes take an offset the check
+  // rejects, so they read zeros with no memory access; their columns are never
+  // stored.  Loop invariant: the step offsets stay scalar.
+  const bool col_in = n0w + 2 * l32 < N;
+  const uint32_t w_lane = col_in ? ((uint32_t)lh * (uint32_t)N + (uint32_t)(n0w + 2 * l32)) * 4u : OOB;
+  const uint32_t sz_col = col_in ? (uint32_t)(n0w + 2 * l32) * 2u : OOB;
   const uint32_t magic = fp16_magic_vgpr();
   // A-fragment read offsets (elements) of block mb = 0: row l32, chunk 2 ks + lh.
   // Block mb adds 32 rows (2048 elements, an immediate offset): its rows have
@@ -502,7 +510,9 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   // The step enters every load through the scalar offset (the per-lane offsets
   // are loop invariant: no per-step vector address arithmetic).  Prefetches
   // past this split's last step, which no step consumes, reload that last
-  // step, so every load stays inside its tensor.
+  // step.  With the columns past N sent out of range above, every load with
+  // an in-range per-lane offset stays inside its tensor (also in a partial
+  // last column tile).
   auto issue = [&](Regs& r, int st) {  // step st (0-based within this split)
     const int kt = kt0 + (st < nsteps ? st : nsteps - 1);  // scalar
     uint16_t* slot = xs + (st & 3) * SLOT;

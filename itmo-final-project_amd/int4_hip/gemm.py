@@ -22,9 +22,9 @@ tiles by timing, gemm.py:161-168).  Every call launches on the caller's
 current stream and never synchronizes.  The split-K workspace is one
 persistent zero-initialised buffer per (device, stream), allocated on the first
 call and never freed (the kernels leave its counters zero); a call captured on a
-stream that has none runs without one when its route needs none, else with a
-graph-private buffer (see ``_with_workspace``), so graphs can be captured with
-or without a warm-up call on the capture stream.
+stream that has none uses one buffer per capture stream, shared by every graph
+captured there (see ``_with_workspace``), so graphs can be captured with or
+without a warm-up call on the capture stream.
 """
 from __future__ import annotations
 
@@ -49,9 +49,11 @@ def _check_weight(qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tens
     return G
 
 
-_WS: dict = {}
-_WS_ALL: list = []
+_WS: dict = {}       # (device, stream) -> persistent zero-initialised workspace
+_CAP_WS: dict = {}   # (device, capture stream) -> workspace of calls captured there
+_WS_RETIRED: list = []  # outgrown buffers, still referenced by captured graphs
 _WS_LOCK = threading.Lock()
+_COUNTER_BYTES = 65536  # W4_WORKSPACE_COUNTER_BYTES
 
 
 def _stream_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor | None:
@@ -69,9 +71,27 @@ def _stream_workspace(device: torch.device, stream: int, nbytes: int) -> torch.T
             return ws
         if torch.cuda.is_current_stream_capturing():
             return None
+        if ws is not None:
+            _WS_RETIRED.append(ws)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _WS_ALL.append(ws)
         _WS[key] = ws
+        return ws
+
+
+def _capture_workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Workspace for a call captured on a stream that has no (large enough)
+    persistent one: one buffer per (device, capture stream), taken from the
+    graph's private pool the first time and replaced only by a larger one, so
+    capturing many graphs on one stream (torch's default capture stream among
+    them) keeps at most one live buffer per size it had to grow to."""
+    key = (device.index, stream)
+    with _WS_LOCK:
+        ws = _CAP_WS.get(key)
+        if ws is None or ws.numel() < nbytes:
+            if ws is not None:
+                _WS_RETIRED.append(ws)  # graphs captured before still use it
+            ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            _CAP_WS[key] = ws
         return ws
 
 
@@ -82,23 +102,19 @@ def _with_workspace(device: torch.device, stream: int, nbytes: int, launch) -> i
 
     A graph may be captured on a stream that never ran an eager call (torch's
     own capture stream, as ``torch.cuda.graph(g)`` without a stream and
-    ``triton.testing.do_bench_cudagraph`` use).  There the call first runs
-    without a workspace: most shapes need none, and the library refuses with
-    W4_ERR_WORKSPACE before launching anything when the route it takes does.
-    Only then is a buffer taken from the graph's private memory, zeroed by a
-    fill kernel that the graph records ahead of the product (so every replay
-    starts from zero counters) and kept for the life of the process."""
+    ``triton.testing.do_bench_cudagraph`` use).  There the call takes the
+    capture stream's buffer (``_capture_workspace``) and records, ahead of the
+    product, a fill kernel (no memset node) that zeroes its counter area: the
+    buffer is shared by every graph captured on that stream and its memory is
+    never written at capture time, so each replay starts from zero counters
+    whichever graph ran last.  Graphs that share a capture stream share its
+    buffer, so their replays must be ordered (as calls on one stream are)."""
     if nbytes == 0:
         return launch(None, 0)
     ws = _stream_workspace(device, stream, nbytes)
-    if ws is not None:
-        return launch(ws.data_ptr(), ws.numel())
-    rc = launch(None, 0)
-    if rc != _lib.ERR_WORKSPACE:
-        return rc
-    ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-    with _WS_LOCK:
-        _WS_ALL.append(ws)
+    if ws is None:
+        ws = _capture_workspace(device, stream, nbytes)
+        ws[:_COUNTER_BYTES].zero_()
     return launch(ws.data_ptr(), ws.numel())
 
 

@@ -23,9 +23,11 @@ Two implementations live here:
 * ``quantize_int4_ref`` / ``unpack_int4_ref`` / ``dequantize_int4_ref``:
   torch-op versions on whatever device the tensors live (CPU included), the
   counterparts of int4_triton/quantize.py:102-135, which the reference's users
-  call to check the kernels.  They are bit-exact with the kernels: every
-  step is an IEEE operation whose result torch fixes (division by 15, not a
-  multiply by its reciprocal; floor of x + 0.5; NaN-propagating extremes).
+  call to check the kernels.  They are bit-exact with the kernels on CPU and
+  GPU tensors alike: every step is an IEEE operation whose result torch
+  fixes on both (division by a 15.0 tensor, never a multiply by its
+  reciprocal; floor of x + 0.5; NaN-propagating extremes; NaN codes mapped to
+  INT32_MIN before the integer cast).
 """
 from __future__ import annotations
 
@@ -112,12 +114,21 @@ def quantize_int4_ref(w: torch.Tensor, group_size: int = 128):
     groups = w.float().unflatten(1, (K // G, G))                 # [N, K/G, G]
     top = torch.clamp(groups.amax(dim=2), min=0.0)
     bottom = torch.clamp(groups.amin(dim=2), max=0.0)
-    step = (top - bottom) / 15.0
+    # divide by a tensor on w's device: torch turns GPU division by a host
+    # scalar into a multiply by its fp32 reciprocal, which differs from the
+    # correctly rounded quotient in the last bit for some ranges
+    fifteen = torch.full((), 15.0, dtype=torch.float32, device=w.device)
+    step = (top - bottom) / fifteen
     step = step.masked_fill(step == 0.0, 1.0).to(torch.float16)  # the stored scale
     step32 = step.float()
     zp = torch.clamp(torch.floor(bottom.neg() / step32 + 0.5), 0.0, 15.0)
     codes = torch.floor(groups / step32.unsqueeze(2) + 0.5).add_(zp.unsqueeze(2))
-    codes = codes.clamp_(0.0, 15.0).to(torch.int32).reshape(N, K // 8, 8)
+    codes = codes.clamp_(0.0, 15.0)
+    # a NaN code (a group holding NaN or both infinities) becomes INT32_MIN, the
+    # value of the x86 truncating conversion the reference's CPU path applies;
+    # the GPU conversion would give 0
+    codes = codes.masked_fill_(codes.isnan(), -2.0**31)
+    codes = codes.to(torch.int32).reshape(N, K // 8, 8)
     words = codes[..., 0].clone()
     for i in range(1, 8):
         words.bitwise_or_(codes[..., i] << _NIBBLE_SHIFTS[i])

@@ -169,3 +169,50 @@ def test_product_package_does_not_import_the_oracle():
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(RuntimeError, match="not built"):
         _lib.load(tmp_path / "nope.so")
+
+
+def _pf3_max_reach(N, K, G, NW, szk, mask_cols):
+    """Model of pf3_tile's weight / scale loads (w4_prefill.hip: w_lane, sz_col
+    and `issue`): for every lane of every column tile and every step (plus the
+    clamped prefetches), the raw-buffer range check rejects a load whose
+    per-lane offset is >= the tensor's bytes, and otherwise the bytes
+    [voffset + soffset, + size) are read.  Returns the largest end reached in
+    qweight and in scales (zeros share the scales' offsets)."""
+    OOB = 0x80000000
+    qw_bytes, sz_bytes = K // 8 * N * 4, K // G * N * 2
+    tiles_n = -(-N // (64 * NW))
+    KT = K // 64
+    reach_q = reach_s = 0
+    for tn in range(tiles_n):
+        for wn in range(NW):
+            n0w = (tn * NW + wn) * 64
+            for lane in range(64):
+                l32, lh = lane & 31, lane >> 5
+                col_in = (n0w + 2 * l32 < N) or not mask_cols
+                w_lane = (lh * N + n0w + 2 * l32) * 4 if col_in else OOB
+                sz_col = (n0w + 2 * l32) * 2 if col_in else OOB
+                for kt in range(KT):  # prefetches past the end reload step KT - 1
+                    for ks in range(4):
+                        if w_lane < qw_bytes:
+                            reach_q = max(reach_q, w_lane + kt * 8 * N * 4 + ks * 2 * N * 4 + 8)
+                    for j in range(4 if szk else 1):
+                        g = (kt * 64 + (j * 16 + lh * 8 if szk else 0)) // G
+                        vo, so = (g * N * 2 + sz_col, 0) if szk else (sz_col, g * N * 2)
+                        if vo < sz_bytes:
+                            reach_s = max(reach_s, vo + so + 4)
+    return (reach_q, qw_bytes), (reach_s, sz_bytes)
+
+
+@pytest.mark.parametrize("N,K,G,NW", [(96, 256, 64, 4), (130, 192, 32, 2), (2050, 128, 128, 4), (64 * 4 + 2, 64, 8, 4)])
+def test_pf3_loads_stay_inside_their_tensors(N, K, G, NW):
+    """N not a multiple of the tile width: the lanes of a partial last tile
+    whose columns lie past N must not read past the end of qweight or scales
+    (the range check sees only the per-lane offset, the step travels in the
+    scalar offset), so a C-ABI caller with exact-size buffers is safe."""
+    for szk in (G < 64, False):
+        (rq, nq), (rs, ns) = _pf3_max_reach(N, K, G, NW, szk, mask_cols=True)
+        assert rq <= nq and rs <= ns, (N, K, G, NW, szk, rq, nq, rs, ns)
+    # the same model without the column mask reaches past the end: the check
+    # above would catch a regression of the mask
+    (rq, nq), _ = _pf3_max_reach(N, K, G, NW, False, mask_cols=False)
+    assert rq > nq

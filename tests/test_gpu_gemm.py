@@ -381,6 +381,38 @@ def test_capture_without_warmup_on_capture_stream(M, N, K, G):
     _replays_match(g, out, eager)
 
 
+# many graphs captured on torch's default capture stream, each with no warm-up
+# and a route that needs the workspace (M = 40 with K = 8192: the decode
+# kernel's K split, partial tiles and arrival counters): the captures share
+# one buffer per (device, capture stream) instead of one each, and every
+# graph, replayed in any order, starts from zero counters
+def test_capture_many_graphs_shares_one_workspace():
+    from int4_hip import gemm as _gemm
+    qw, s, z = _weights(2048, 8192, 128, seed=77)
+    x = randn((40, 8192), seed=78).to(DEV)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        eager = int4_hip.w4a16_matmul(x, qw, s, z)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    def buffers():
+        return {t.data_ptr() for t in list(_gemm._WS.values()) + list(_gemm._CAP_WS.values()) + _gemm._WS_RETIRED}
+
+    before = buffers()
+    graphs = []
+    for i in range(20):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = int4_hip.w4a16_matmul(x, qw, s, z)
+        graphs.append((g, out))
+    assert len(buffers() - before) <= 1, "captured calls must share the capture stream's workspace"
+    order = list(range(19, -1, -1)) + [0, 7, 3, 19, 7]
+    for i in order:
+        _replays_match(graphs[i][0], graphs[i][1], eager, reps=1)
+
+
 def test_capture_grouped_without_warmup():
     shapes = [(2048, 2048), (512, 2048), (512, 2048), (2048, 8192)]
     ws = [_weights(N, K, 32 if i == 3 else 128, seed=500 + i) for i, (N, K) in enumerate(shapes)]
