@@ -71,8 +71,11 @@ struct DecArgs {
   int ksplit;
   unsigned long long* pair;
   // 16-row launches: M may exceed 16; the problem is then cut into `slices`
-  // row slices of 16, workgroup tile t covering column tile t % col_tiles of
-  // rows [16 s, 16 s + 16), s = t / col_tiles (see dec_row_slice)
+  // row slices of 16, workgroup t covering column tile (and K part)
+  // t % col_tiles of slice t / col_tiles (dec_kernel_slices; dec_kernel via
+  // dec_row_slice).
+  // dec_kernel: workgroup t covers column tile t % col_tiles of rows
+  // [16 s, 16 s + 16), s = t / col_tiles (see dec_row_slice).
   int slices;
   int col_tiles;
   // M > 1, ksplit > 1: per column tile one arrival counter (zero on entry
@@ -581,8 +584,10 @@ __device__ __forceinline__ void dec_split_finish(const DecArgs& a, const float* 
   }
 }
 
-template <int DT, int TW, int GSI, int NL, int D, int MR>
-__device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t* lds) {
+// WV: waves of the workgroup.  sl0: the 16-row slice of the problem this
+// workgroup computes (the eight-wave sixteen-row kernel; otherwise 0)
+template <int DT, int TW, int GSI, int NL, int D, int MR, int WV = kOneWaves>
+__device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t* lds, int sl0 = 0) {
   typedef typename Act<DT>::frag F;
   typedef DecNum<DT> Num;
   constexpr int RPS = TW == 128 ? 2 : TW == 64 ? 4 : 8;  // qweight rows per load step
@@ -634,7 +639,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     oq = lane & 7;
     part = lane >= 40 ? 1 : 0;
   }
-  const int N = a.N, K = a.K, M = MR == 1 ? 1 : a.M;
+  const int N = a.N, K = a.K;
   // K split (64-column tiles only when M > 1): column tile ct, part kp of ks,
   // steps [s0, s0 + S); ks is a power of two, so shifts replace the integer
   // divisions (the prologue before the first load is on every workgroup's
@@ -646,9 +651,12 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   const int n0 = ct * TW;
   const int S = (int)((unsigned)K / (unsigned)SK) >> ks_log;
   const int s0 = kp * S;
-  const int per_wave = ((S + kOneWaves - 1) / kOneWaves + NL - 1) / NL * NL;
+  const int per_wave = ((S + WV - 1) / WV + NL - 1) / NL * NL;
   const int wb = s0 + min(S, wv * per_wave);
   const int we = s0 + min(S, min(S, wv * per_wave) + per_wave);
+  // Row slices (problems of more than 16 rows): the workgroup computes its
+  // column tile (or K part) for rows [16 sl0, 16 sl0 + 16) of the problem.
+  auto rows_of = [&](int sl) { return MR == 1 ? 1 : MR == 16 ? min(16, a.M - 16 * sl) : a.M; };
 
   const __amdgpu_buffer_rsrc_t rq =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, kDecBufFlags);
@@ -656,22 +664,40 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, kDecBufFlags);
   const __amdgpu_buffer_rsrc_t rz =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, kDecBufFlags);
-  const __amdgpu_buffer_rsrc_t rx =
-      __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kDecBufFlags);
+  // activations of slice sl: rows [16 sl, 16 sl + rows_of(sl)) (one slice: the
+  // problem's range)
+  auto x_rsrc = [&](int sl) {
+    if (MR < 16 || a.slices == 1)
+      return __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kDecBufFlags);
+    const int64_t r0 = 16 * (int64_t)sl;
+    const int xb = (int)(((int64_t)(rows_of(sl) - 1) * a.sxm + K) * 2);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + r0 * a.sxm), (short)0, xb, kDecBufFlags);
+  };
 
   const uint32_t step_bytes = (uint32_t)RPS * 4u * (uint32_t)N;
   const uint32_t w_lane = ((uint32_t)lr * (uint32_t)N + (uint32_t)(n0 + 4 * lq)) * 4u;
   // activation entry f = 64 j + lane of a round: row f / XE, entry f % XE
-  // (k8 row sb * RPS + f % XE); entries of rows past M read zeros
+  // (k8 row sb * RPS + f % XE); entries of rows past the slice's rows read zeros
   uint32_t x_lane[XLD];
+  auto set_x_lanes = [&](int rows) {
 #pragma unroll
-  for (int j = 0; j < XLD; ++j) {
-    const int f = 64 * j + lane, m = f / XE, e = f % XE;
-    x_lane[j] = (f < MR * XE && m < M) ? ((uint32_t)m * (uint32_t)a.sxm + (uint32_t)e * 8u) * 2u : kDecOOB;
-  }
+    for (int j = 0; j < XLD; ++j) {
+      const int f = 64 * j + lane, m = f / XE, e = f % XE;
+      x_lane[j] = (f < MR * XE && m < rows) ? ((uint32_t)m * (uint32_t)a.sxm + (uint32_t)e * 8u) * 2u : kDecOOB;
+    }
+  };
+  set_x_lanes(rows_of(sl0));
   const uint32_t sz_oob = lane < NP * LPG ? 0u : kDecOOB;
   const uint32_t sz_lane = (uint32_t)(lane / LPG) * (uint32_t)N * 2u + (uint32_t)(n0 * 2 + (lane % LPG) * 16);
   uint8_t* x_lds = lds + wv * WLDS;
+  // Activation staging: row m holds NL * SLOTS 16-byte chunks, chunk c (step
+  // c / SLOTS, k slot c % SLOTS) stored at position c ^ (m % MR) of the row.
+  // An A-fragment read serves 16 lanes with the same chunk of up to 16
+  // different rows; rows are NL * SLOTS * 16 bytes apart (a multiple of the
+  // 256-byte bank line), so without the XOR they would all hit the same four
+  // banks (a 16-way conflict at sixteen rows); with it they cover distinct
+  // bank quads.
+  auto xpos = [&](int m, int c) { return (m * (NL * SLOTS) + (c ^ (m & (MR - 1)))) * 16; };
   uint8_t* s_lds = x_lds + MR * one_xrow(MR);
   uint8_t* z_lds = s_lds + 1024;
   const uint32_t magic = dec_magic_vgpr<DT>();
@@ -681,7 +707,7 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
 #pragma unroll
     for (int f = lane; f < 2 * NL * MR; f += 64) {
       const int m = f / (2 * NL), e = f % (2 * NL);
-      *reinterpret_cast<u32x4*>(x_lds + ((m * NL + (e >> 1)) * SLOTS + 2 + (e & 1)) * 16) = u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(x_lds + xpos(m, (e >> 1) * SLOTS + 2 + (e & 1))) = u32x4{0u, 0u, 0u, 0u};
     }
   }
 
@@ -689,13 +715,17 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     u32x4 w[NL];
     u32x4 x[XLD], s, z;
   };
+  auto load_x = [&](Round& r, __amdgpu_buffer_rsrc_t rx, int sb) {
+    const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
+#pragma unroll
+    for (int j = 0; j < XLD; ++j)
+      r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (x_lane[j] + (uint32_t)sb * RPS * 16u) | oob, 0, 0);
+  };
   // Issue order = order of use: activations, scales, zeros, weights.
   auto load_round = [&](Round& r, int sb) {
     const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < XLD; ++j)
-      r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (x_lane[j] + (uint32_t)sb * RPS * 16u) | oob, 0, 0);
+    load_x(r, x_rsrc(sl0), sb);
     const uint32_t g0 = (uint32_t)((sb * SK) >> a.gshift);
     const uint32_t so = (g0 * (uint32_t)N * 2u + sz_lane) | sz_oob | oob;
     r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, kDecWeightAux);
@@ -711,29 +741,29 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   f32x4 acc[4];
   f32x4 xs;
   float tot[4][RE];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int e = 0; e < RE; ++e) tot[j][e] = 0.f;
 
-  auto compute_round = [&](const Round& r, int sb) {
-    // stage the round's activations (permuted), scales and zeros
+  // stage the round's activations (permuted) and, with_sz, its scales and zeros
+  auto stage_round = [&](const Round& r, bool with_sz) {
 #pragma unroll
     for (int j = 0; j < XLD; ++j) {
       const int f = 64 * j + lane, m = f / XE, e = f % XE;
       if (f < MR * XE)
-        *reinterpret_cast<u32x4*>(x_lds + ((m * NL + e / RPS) * SLOTS + e % RPS) * 16) = dec_perm_x(r.x[j]);
+        *reinterpret_cast<u32x4*>(x_lds + xpos(m, (e / RPS) * SLOTS + e % RPS)) = dec_perm_x(r.x[j]);
     }
-    *reinterpret_cast<u32x4*>(s_lds + lane * 16) = r.s;
-    *reinterpret_cast<u32x4*>(z_lds + lane * 16) = r.z;
+    if (with_sz) {
+      *reinterpret_cast<u32x4*>(s_lds + lane * 16) = r.s;
+      *reinterpret_cast<u32x4*>(z_lds + lane * 16) = r.z;
+    }
     __builtin_amdgcn_wave_barrier();
+  };
+  auto compute_round = [&](const Round& r, int sb) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
 #pragma unroll
       for (int i = 0; i < GS; ++i) {
         const int st = p * GS + i;
         const F xa = __builtin_bit_cast(
-            F, *reinterpret_cast<const u32x4*>(x_lds + ((a_row * NL + st) * SLOTS + a_slot) * 16));
+            F, *reinterpret_cast<const u32x4*>(x_lds + xpos(a_row, st * SLOTS + a_slot)));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const F b = __builtin_bit_cast(F, Num::bvals(r.w[st][j], magic));
@@ -758,25 +788,12 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     }
     __builtin_amdgcn_wave_barrier();  // the next round rewrites the staging area
   };
-
-  if constexpr (D == 1) {
-    // the host picks D == 1 only when a wave's run fits in one round
-    if (wb < we) {
-      Round r;
-      load_round(r, wb);
-      compute_round(r, wb);
-    }
-  } else {
-    Round ra, rb;
-    load_round(ra, wb);
-    load_round(rb, wb + NL);
-    for (int sb = wb; sb < we; sb += 2 * NL) {
-      compute_round(ra, sb);
-      load_round(ra, sb + 2 * NL);
-      if (sb + NL < we) compute_round(rb, sb + NL);
-      load_round(rb, sb + 3 * NL);
-    }
-  }
+  auto clear_tot = [&]() {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < RE; ++e) tot[j][e] = 0.f;
+  };
 
   // cross-wave (T32: and even/odd row) reduction in a fixed order; partials
   // of wave w, row m at red + w * RSTR + m * 128
@@ -784,89 +801,188 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   constexpr int RSTR = MR >= 8 ? WLDS / 4 : MR * 128;  // floats
   constexpr int RROW = MR == 16 ? 64 : 128;
   float* red = reinterpret_cast<float*>(lds + (MR >= 8 ? 0 : one_red_offset(MR)));
-  if (owner) {
+
+  // Reduce the workgroup's partials of slice sl and store them (or, K split
+  // with several rows, publish them; the last part to arrive stores the sum).
+  auto finish_slice = [&](int sl) {
+    const int M = rows_of(sl);
+    uint16_t* const y = a.y + (int64_t)(16 * sl) * a.ldy;
+    if (owner) {
+      // the four columns of an output quad as one 16-byte store per row
 #pragma unroll
-    for (int e = 0; e < RE; ++e)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) red[wv * RSTR + (r_base + e) * RROW + part * 32 + 4 * oq + j] = tot[j][e];
-  }
-  __syncthreads();
-  if constexpr (MR == 1 && TW % 64 == 0) {
-    if (ks > 1) {
-      if (wv == 0) dec_split_finish<DT, TW, RSTR>(a, red, ct, kp, ks, n0, lane);
-      return;
+      for (int e = 0; e < RE; ++e)
+        *reinterpret_cast<f32x4*>(&red[wv * RSTR + (r_base + e) * RROW + part * 32 + 4 * oq]) =
+            f32x4{tot[0][e], tot[1][e], tot[2][e], tot[3][e]};
     }
-  }
-  if constexpr (MR > 1 && TW == 64) {
-    if (ks > 1) {
-      // Several rows, K split: each part publishes its MR x 64 partial tile
-      // with device-coherent stores (sc1: written through to the point all
-      // XCDs read from), waits until they have completed and bumps the
-      // tile's counter; the part that arrives last reads the others' tiles
-      // with device-coherent loads, sums all parts in part order (so the
-      // result does not depend on which part is last) and writes y, then
-      // leaves the counter at zero.  Thread tid < MR * TW owns element tid
-      // of the tile.
-      constexpr int E = MR * TW;
-      static_assert(E <= kOneThreads, "one tile element per thread");
-      const int m = tid / TW, nl = tid - m * TW;
-      float* const tiles = a.part + (int64_t)ct * ks * E;
-      float v = 0.0f;
-      if (tid < E) {
-        float pv[kOneWaves];
+    __syncthreads();
+    // Eight-wave sixteen-row kernel: each thread reduces two adjacent columns
+    // of one row (64-bit LDS reads; the same adds in the same order as one
+    // column per thread), so the tail is one round of reads for 512 threads.
+    constexpr bool PAIR = MR * TW == 2 * WV * 64;
+    if constexpr (PAIR) {
+      const int el = 2 * tid, m = el / TW, nl = el - m * TW;
+      float2 pv[WV];
 #pragma unroll
-        for (int w = 0; w < kOneWaves; ++w) pv[w] = red[w * RSTR + m * RROW + nl];
-#pragma unroll
-        for (int w = 0; w < kOneWaves; ++w) v += pv[w];
-        __hip_atomic_store(tiles + kp * E + tid, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();  // every partial of this part has completed; red is no longer read
-      unsigned* const arrived = reinterpret_cast<unsigned*>(lds);
-      if (tid == 0) *arrived = __hip_atomic_fetch_add(a.cnt + ct, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      if (*arrived != (unsigned)(ks - 1)) return;
-      if (tid == 0) __hip_atomic_store(a.cnt + ct, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (tid >= E) return;
-      float other[kMaxKSplit];
-#pragma unroll
-      for (int p = 0; p < kMaxKSplit; ++p)
-        other[p] = (p < ks && p != kp)
-                       ? __hip_atomic_load(tiles + p * E + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : v;
-      float sum = 0.0f;
-#pragma unroll
-      for (int p = 0; p < kMaxKSplit; ++p)
-        if (p < ks) sum += other[p];
-      const int n = n0 + nl;
-      if (m < M && n < N) a.y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(sum * (1.0f / Num::QS));
-      return;
-    }
-  }
-  if (tid < MR * TW) {
-    const int m = tid / TW, nl = tid - m * TW;
-    const int n = n0 + nl;
-    if (m < M && n < N) {
-      // every partial is read before the first add (one LDS latency instead
-      // of one per few reads); the adds keep the wave order
-      constexpr int NPART = TW == 32 ? 2 * kOneWaves : kOneWaves;
-      float pv[NPART];
-#pragma unroll
-      for (int w = 0; w < kOneWaves; ++w) {
-        const float* rw = red + w * RSTR + m * RROW;
-        if constexpr (TW == 32) {
-          pv[2 * w] = rw[nl];
-          pv[2 * w + 1] = rw[32 + nl];
-        } else {
-          pv[w] = rw[nl];
-        }
-      }
+      for (int w = 0; w < WV; ++w) pv[w] = *reinterpret_cast<const float2*>(&red[w * RSTR + m * RROW + nl]);
       __builtin_amdgcn_sched_barrier(0);
-      float v = 0.0f;
+      float vx = 0.0f, vy = 0.0f;
 #pragma unroll
-      for (int i = 0; i < NPART; ++i) v += pv[i];
-      a.y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(v * (1.0f / Num::QS));
+      for (int w = 0; w < WV; ++w) vx += pv[w].x, vy += pv[w].y;
+      const int n = n0 + nl;  // N % 8 == 0 on this kernel: n and n + 1 are both inside or both past N
+      if (ks > 1) {
+        // K split: publish the pair (one 64-bit device-coherent store), count
+        // the part's arrival; the last part sums every part in part order
+        constexpr int E = MR * TW;
+        unsigned* const cnt = a.cnt + (int64_t)sl * (a.col_tiles >> ks_log);
+        float* const tiles = a.part + (int64_t)sl * a.col_tiles * E + (int64_t)ct * ks * E;
+        const unsigned long long mine =
+            (unsigned long long)__builtin_bit_cast(uint32_t, vx) | ((unsigned long long)__builtin_bit_cast(uint32_t, vy) << 32);
+        __hip_atomic_store(reinterpret_cast<unsigned long long*>(tiles + kp * E + el), mine, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // every partial of this part has completed; red is no longer read
+        unsigned* const arrived = reinterpret_cast<unsigned*>(lds);
+        if (tid == 0) *arrived = __hip_atomic_fetch_add(cnt + ct, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*arrived != (unsigned)(ks - 1)) return;
+        if (tid == 0) __hip_atomic_store(cnt + ct, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        unsigned long long other[kMaxKSplit];
+#pragma unroll
+        for (int q = 0; q < kMaxKSplit; ++q)
+          other[q] = (q < ks && q != kp)
+                         ? __hip_atomic_load(reinterpret_cast<unsigned long long*>(tiles + q * E + el), __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT)
+                         : mine;
+        vx = 0.0f, vy = 0.0f;
+#pragma unroll
+        for (int q = 0; q < kMaxKSplit; ++q)
+          if (q < ks) {
+            vx += __builtin_bit_cast(float, (uint32_t)other[q]);
+            vy += __builtin_bit_cast(float, (uint32_t)(other[q] >> 32));
+          }
+      }
+      if (m < M && n < N) {
+        y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(vx * (1.0f / Num::QS));
+        y[(int64_t)m * a.ldy + n + 1] = float_to_act_bits<DT>(vy * (1.0f / Num::QS));
+      }
+      return;
     }
+    if constexpr (MR == 1 && TW % 64 == 0) {
+      if (ks > 1) {
+        if (wv == 0) dec_split_finish<DT, TW, RSTR>(a, red, ct, kp, ks, n0, lane);
+        return;
+      }
+    }
+    if constexpr (MR > 1 && TW == 64) {
+      if (ks > 1) {
+        // Several rows, K split: each part publishes its MR x 64 partial tile
+        // with device-coherent stores (sc1: written through to the point all
+        // XCDs read from), waits until they have completed and bumps the
+        // tile's counter; the part that arrives last reads the others' tiles
+        // with device-coherent loads, sums all parts in part order (so the
+        // result does not depend on which part is last) and writes y, then
+        // leaves the counter at zero.  Thread tid < MR * TW owns element tid
+        // of the tile.  Slice sl has its own counters and partial tiles.
+        constexpr int E = MR * TW;
+        constexpr int EPT = (E + WV * 64 - 1) / (WV * 64);  // tile elements per thread
+        unsigned* const cnt = a.cnt + (int64_t)sl * (a.col_tiles >> ks_log);
+        float* const tiles = a.part + (int64_t)sl * a.col_tiles * E + (int64_t)ct * ks * E;
+        float v[EPT];
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) {
+          const int el = tid + i * WV * 64, m = el / TW, nl = el - m * TW;
+          v[i] = 0.0f;
+          if (el < E) {
+            float pv[WV];
+#pragma unroll
+            for (int w = 0; w < WV; ++w) pv[w] = red[w * RSTR + m * RROW + nl];
+#pragma unroll
+            for (int w = 0; w < WV; ++w) v[i] += pv[w];
+            __hip_atomic_store(tiles + kp * E + el, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();  // every partial of this part has completed; red is no longer read
+        unsigned* const arrived = reinterpret_cast<unsigned*>(lds);
+        if (tid == 0) *arrived = __hip_atomic_fetch_add(cnt + ct, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (*arrived == (unsigned)(ks - 1)) {
+          if (tid == 0) __hip_atomic_store(cnt + ct, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+          for (int i = 0; i < EPT; ++i) {
+            const int el = tid + i * WV * 64, m = el / TW, nl = el - m * TW;
+            if (el < E) {
+              float other[kMaxKSplit];
+#pragma unroll
+              for (int p = 0; p < kMaxKSplit; ++p)
+                other[p] = (p < ks && p != kp)
+                               ? __hip_atomic_load(tiles + p * E + el, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : v[i];
+              float sum = 0.0f;
+#pragma unroll
+              for (int p = 0; p < kMaxKSplit; ++p)
+                if (p < ks) sum += other[p];
+              const int n = n0 + nl;
+              if (m < M && n < N) y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(sum * (1.0f / Num::QS));
+            }
+          }
+        }
+        return;
+      }
+    }
+    for (int el = tid; el < MR * TW; el += WV * 64) {
+      const int m = el / TW, nl = el - m * TW;
+      const int n = n0 + nl;
+      if (m < M && n < N) {
+        // every partial is read before the first add (one LDS latency instead
+        // of one per few reads); the adds keep the wave order
+        constexpr int NPART = TW == 32 ? 2 * WV : WV;
+        float pv[NPART];
+#pragma unroll
+        for (int w = 0; w < WV; ++w) {
+          const float* rw = red + w * RSTR + m * RROW;
+          if constexpr (TW == 32) {
+            pv[2 * w] = rw[nl];
+            pv[2 * w + 1] = rw[32 + nl];
+          } else {
+            pv[w] = rw[nl];
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        float v = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPART; ++i) v += pv[i];
+        y[(int64_t)m * a.ldy + n] = float_to_act_bits<DT>(v * (1.0f / Num::QS));
+      }
+    }
+  };
+
+  if constexpr (D == 1) {
+    // the host picks D == 1 only when a wave's run fits in one round
+    clear_tot();
+    if (wb < we) {
+      Round r;
+      load_round(r, wb);
+      stage_round(r, true);
+      compute_round(r, wb);
+    }
+    finish_slice(sl0);
+  } else {
+    clear_tot();
+    Round ra, rb;
+    load_round(ra, wb);
+    load_round(rb, wb + NL);
+    for (int sb = wb; sb < we; sb += 2 * NL) {
+      stage_round(ra, true);
+      compute_round(ra, sb);
+      load_round(ra, sb + 2 * NL);
+      if (sb + NL < we) {
+        stage_round(rb, true);
+        compute_round(rb, sb + NL);
+      }
+      load_round(rb, sb + 3 * NL);
+    }
+    finish_slice(0);
   }
 }
 
@@ -907,12 +1023,48 @@ __global__ __launch_bounds__(kOneThreads) void dec_kernel_one(DecGroupedArgs g) 
       case kCfgT64: dec_tile_one<DT, 64, G64, 8, 1, MR>(a, tile, lds); break;
       default: dec_tile_one<DT, 32, G32, 8, 1, MR>(a, tile, lds); break;
     }
-  } else {
-    // sixteen rows: the 64-column tiling only, problems of more rows in slices
-    int st = tile;
-    const DecArgs as = dec_row_slice(a, st);
-    dec_tile_one<DT, 64, G64, 8, 1, MR>(as, st, lds);
   }
+}
+
+// Problems of more than 16 rows (17 <= M <= 128), one 16-row slice per
+// workgroup: eight waves over 64-column tiles and K parts of at most 2048 (8
+// waves x 8 steps of 32 k), 80 KB of LDS and at most 128 VGPRs, so that two
+// workgroups share a CU and one's memory wait overlaps the other's
+// arithmetic.  (The sixteen-wave kernel leaves half of its waves idle at
+// K = 2048 and holds the whole LDS, one workgroup per CU: the grouped
+// decoder block at M = 64 took 37.7 us on it.)
+constexpr int kSliceWaves = 8;
+template <int DT, int GC>
+__global__ __launch_bounds__(64 * kSliceWaves) __attribute__((amdgpu_waves_per_eu(4))) void dec_kernel_slices(
+    DecGroupedArgs g) {
+  __shared__ __attribute__((aligned(16))) float dec_smem[kSliceWaves * one_wave_lds(16) / 4];
+  const int t = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < W4_MAX_GROUPED; ++i)
+    if (i < g.count && t >= g.wg_start[i]) p = i;
+  const DecArgs& a = g.prob[p];
+  const int tile = t - g.wg_start[p];
+  constexpr int G64 = 1 << GC;
+  // Workgroup order: blocks of 8 column tiles x all slices, slice-major
+  // inside a block, so the slices of one column tile are dispatched within
+  // 8 * slices consecutive workgroups, all to the same XCD (workgroups go to
+  // the XCDs round-robin and 8 divides the block stride): their reads of the
+  // tile's weights meet in that XCD's L2 at about the same time.  Column
+  // tiles past the last whole block of 8 follow, slice-major.
+  const int S = a.slices, T = a.col_tiles;
+  const int full = T & ~7;
+  int sl, ct;
+  if (tile < full * S) {
+    const int blk = tile / (8 * S), r = tile - blk * 8 * S;
+    sl = r >> 3;
+    ct = blk * 8 + (r & 7);
+  } else {
+    const int rem = T - full, r = tile - full * S;
+    sl = r / rem;
+    ct = full + (r - sl * rem);
+  }
+  dec_tile_one<DT, 64, G64, 8, 1, 16, kSliceWaves>(a, ct, reinterpret_cast<uint8_t*>(dec_smem), sl);
 }
 
 template <int DT, bool ONE, int GS, int MX>
@@ -963,6 +1115,7 @@ struct DecPlan {
   int gs;         // group-size class of the chosen kernel
   int mx;         // dec_kernel, M > 1: activation rows staged per wave (4, 8 or 16)
   bool cu_tiles;  // M == 1 one-workgroup-per-CU kernel (dec_kernel_one)
+  bool sliced;    // cu_tiles with problems of more than 16 rows (dec_kernel_slices)
   int threads;
   size_t lds;
   // K-split problems (M == 1): their pairing words, as 64-bit word offsets
@@ -986,13 +1139,18 @@ struct DecPlan {
 // exists.
 // `deeper` halves the parts again that many times while they stay whole
 // groups and rounds: a lone down_proj at M = 16 has only 32 column tiles.
-int sixteen_ksplit(int64_t K, int G, int deeper = 0) {
-  if (K <= 4096) return 1;
+//
+// Every several-row kernel runs rounds of 8 steps (256 k) per wave: one round
+// of the sixteen-wave kernels holds K <= 4096, one of the eight-wave kernel
+// for problems of more than 16 rows K <= 2048 (`part`).
+int sixteen_ksplit(int64_t K, int G, int deeper, int64_t part) {
+  const int64_t round = 256;
+  if (K <= part) return 1;
   auto ok = [&](int k) {
-    return k <= w4::kMaxKSplit && K % k == 0 && (K / k) % 256 == 0 && (K / k) % G == 0;
+    return k <= w4::kMaxKSplit && K % k == 0 && (K / k) % round == 0 && (K / k) % G == 0;
   };
   int ks = 2;
-  while (K / ks > 4096) ks *= 2;
+  while (K / ks > part) ks *= 2;
   if (!ok(ks)) return 0;
   for (int d = 0; d < deeper && ok(2 * ks); ++d) ks *= 2;
   return ks;
@@ -1037,7 +1195,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   struct Item {
     int idx;
     int vec, cfg, tile_n;
-    int64_t tiles, bytes_per_wg;
+    int64_t tiles, bytes_per_wg;  // tiles: column tiles x K parts
     int ks, slices;
   } items[W4_MAX_GROUPED];
   int gclass = -1;
@@ -1045,6 +1203,10 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
   // only the single-round ones: K <= 8192, and K <= 4096 for group 32; for
   // M > 8 only the 64-column one: K <= 4096)
   bool cu_tiles = M <= 16;
+  // sixteen-row launches (9 <= M <= 16, and problems of more rows in 16-row
+  // slices): the eight-wave kernel, K parts <= 2048
+  const bool sliced = M > 8;
+  const int64_t part_k = sliced ? 2048 : 4096;
   for (int i = 0; i < count; ++i) {
     const w4a16_problem& q = problems[i];
     if (!dec_fits_32bit(q.N, q.K) || q.group_size < 32 || !is_pow2(q.group_size)) return false;
@@ -1059,10 +1221,10 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     if (ldy != nullptr && ldy[i] < q.N) return false;
     const uintptr_t qa = (uintptr_t)q.qweight, sa = (uintptr_t)q.scales, za = (uintptr_t)q.zeros;
     cu_tiles = cu_tiles && q.N % 8 == 0 && qa % 16 == 0 && sa % 16 == 0 && za % 16 == 0;
-    const bool split_ok = split16 && sixteen_ksplit(q.K, q.group_size) > 1;
+    const bool split_ok = split16 && sixteen_ksplit(q.K, q.group_size, 0, part_k) > 1;
     if (M > 1 && M <= 8)
       cu_tiles = cu_tiles && ((q.K <= 8192 && (q.group_size >= 64 || q.K <= 4096)) || split_ok);
-    if (M > 8) cu_tiles = cu_tiles && (q.K <= 4096 || split_ok);
+    if (M > 8) cu_tiles = cu_tiles && (q.K <= part_k || split_ok);
   }
   const int G = problems[0].group_size;
   // M == 1 tile width: about 128 KB of packed weights per workgroup (128
@@ -1105,7 +1267,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
         for (int i = 0; i < count; ++i) {
           const w4a16_problem& q = problems[i];
           const int64_t Mi = mrows != nullptr ? mrows[i] : M;
-          const int k = sixteen_ksplit(q.K, q.group_size, d);
+          const int k = sixteen_ksplit(q.K, q.group_size, d, part_k);
           t += (k > 1 ? (q.N + 63) / 64 * k : tiles_at(q, level)) * ((Mi + M - 1) / M);
         }
         return t;
@@ -1132,7 +1294,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
       vec = 4;
       // (sixteen_ksplit returns 0 where no split exists: those problems stay
       // whole, on the single-round tilings)
-      ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : split16 ? std::max(1, sixteen_ksplit(q.K, G, deeper)) : 1;
+      ks = M == 1 ? one_ksplit(q.K, G, level, q.N) : split16 ? std::max(1, sixteen_ksplit(q.K, G, deeper, part_k)) : 1;
       tn = ks > 1 ? 64 : one_width(q.K, level);
       cfg = tn == 128 ? w4::kCfgT128
           : tn == 64  ? (q.K / ks <= 4096 ? w4::kCfgT64 : w4::kCfgT64Ring)
@@ -1144,7 +1306,7 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     }
     const int64_t Mi = mrows != nullptr ? mrows[i] : M;
     const int slices = (int)((Mi + M - 1) / M);  // > 1 only for 16-row launches
-    items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn * ks * slices, (int64_t)tn * (q.K / ks) / 2, ks, slices};
+    items[i] = Item{i, vec, cfg, tn, (q.N + tn - 1) / tn * ks, (int64_t)tn * (q.K / ks) / 2, ks, slices};
   }
   // Longest-running workgroups first: more bytes, then longer K (narrower
   // tiles with more correction points per byte).
@@ -1177,31 +1339,32 @@ bool dec_plan(const w4a16_problem* problems, const int64_t* sxm, const int64_t* 
     a.ksplit = it.ks;
     a.pair = nullptr;
     a.slices = it.slices;
-    a.col_tiles = (int)(it.tiles / it.slices);
+    a.col_tiles = (int)it.tiles;
     a.cnt = nullptr;
     a.part = nullptr;
     if (it.ks > 1 && M > 1) {
       const int mr = M <= 4 ? 4 : M <= 8 ? 8 : 16;  // rows of the launch's kernel
       dp.cnt_off[s] = dp.cnt_words;
       dp.part_off[s] = dp.part_floats;
-      dp.cnt_words += it.tiles / it.ks;
-      dp.part_floats += it.tiles * mr * 64;
+      dp.cnt_words += it.tiles / it.ks * it.slices;  // per slice: one counter per column tile
+      dp.part_floats += it.tiles * it.slices * mr * 64;
     }
     if (it.ks > 1 && M == 1) {
       dp.pair_off[s] = dp.pair_words;
       dp.pair_words += (it.tiles / it.ks) * (it.ks - 1) * it.tile_n;
     }
     dp.g.wg_start[s] = wgs;
-    if (it.tiles > (1 << 24)) return false;
-    wgs += (int)it.tiles;
+    if (it.tiles * it.slices > (1 << 24)) return false;
+    wgs += (int)(it.tiles * it.slices);
   }
   for (int s = count; s <= W4_MAX_GROUPED; ++s) dp.g.wg_start[s] = wgs;
   dp.g.count = count;
   dp.wgs = wgs;
   dp.cu_tiles = cu_tiles;
+  dp.sliced = cu_tiles && sliced;
   if (cu_tiles) {
     dp.gs = std::min(ilog2(G) - 5, 4);  // dec_kernel_one: log2(group / 32), 4 = ">= 512"
-    dp.threads = w4::kOneThreads;
+    dp.threads = sliced ? 64 * w4::kSliceWaves : w4::kOneThreads;
     dp.lds = 0;  // static in dec_kernel_one
   } else {
     dp.gs = (int)std::min(G / 32, 8);  // dec_kernel: steps per group, capped at 8
@@ -1236,15 +1399,27 @@ void dec_launch_one_mr(const DecPlan& dp, hipStream_t st) {
 }
 
 template <int DT>
+void dec_launch_slices(const DecPlan& dp, hipStream_t st) {
+  const dim3 grid((unsigned)dp.wgs), block(64 * w4::kSliceWaves);
+  switch (dp.gs) {
+    case 0: hipLaunchKernelGGL((w4::dec_kernel_slices<DT, 0>), grid, block, 0, st, dp.g); break;
+    case 1: hipLaunchKernelGGL((w4::dec_kernel_slices<DT, 1>), grid, block, 0, st, dp.g); break;
+    case 2: hipLaunchKernelGGL((w4::dec_kernel_slices<DT, 2>), grid, block, 0, st, dp.g); break;
+    case 3: hipLaunchKernelGGL((w4::dec_kernel_slices<DT, 3>), grid, block, 0, st, dp.g); break;
+    default: hipLaunchKernelGGL((w4::dec_kernel_slices<DT, 4>), grid, block, 0, st, dp.g); break;
+  }
+}
+
+template <int DT>
 void dec_launch_one(const DecPlan& dp, int64_t M, hipStream_t st) {
-  if (M == 1)
+  if (dp.sliced)
+    dec_launch_slices<DT>(dp, st);
+  else if (M == 1)
     dec_launch_one_mr<DT, 1>(dp, st);
   else if (M <= 4)
     dec_launch_one_mr<DT, 4>(dp, st);
-  else if (M <= 8)
-    dec_launch_one_mr<DT, 8>(dp, st);
   else
-    dec_launch_one_mr<DT, 16>(dp, st);
+    dec_launch_one_mr<DT, 8>(dp, st);
 }
 
 template <int DT, bool ONE, int MX>
