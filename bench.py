@@ -570,15 +570,24 @@ def main() -> int:
         del src, dst
 
     # ------------------------------------------------- quantize kernel (load time)
-    q_ms = None
+    q_ms = q7_ms = None
     q_bytes = sum(2 * N * K + N * K // 2 + 4 * N * K // G for _, N, K in LINEARS)
     if "quantize" in only:
+        # the block's 7 weights as one grouped launch (w4_quantize_grouped),
+        # and as 7 launches (one quantize_int4 per linear, the reference's
+        # per-module conversion)
         def quant_set(i):
+            return lambda: int4_hip.quantize_int4_grouped(w16[i], G)
+
+        def quant_set7(i):
             return lambda: [int4_hip.quantize_int4(w, G) for w in w16[i]]
 
         gq = graph_of(lambda: [quant_set(i)() for i in range(nsets)], stream)
         q_ms = time_graph(gq, 3, stream) / nsets
         del gq
+        gq7 = graph_of(lambda: [quant_set7(i)() for i in range(nsets)], stream)
+        q7_ms = time_graph(gq7, 3, stream) / nsets
+        del gq7
     # the first set's bf16 weights, kept on the host for the CPU quantize baseline
     w16_host = [w.cpu() for w in w16[0]] if ("quantize" in only and not args.no_cpu) else None
     del w16
@@ -897,6 +906,7 @@ def main() -> int:
         "prefill_m2048_mfma_frac": round(pre[2048]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4) if pre else None,
         "quantize_us_per_block": round(q_ms * 1e3, 2) if q_ms else None,
         "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None,
+        "quantize_7_launches_us_per_block": round(q7_ms * 1e3, 2) if q7_ms else None,
         "cpu_baseline_quantize": cpu_q,
         "hbm_device_copy_gbps": round(copy_gbps, 1) if copy_gbps else None,
         "hbm_read_ceiling": read_ceiling,

@@ -71,6 +71,33 @@ int w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K,
                 int32_t* qweight, uint16_t* scales, uint16_t* zeros, void* stream);
 
 /*
+ * One weight of a grouped quantize call (w4_quantize's arguments).
+ */
+typedef struct w4_quantize_problem {
+  const void* w;
+  int32_t* qweight;
+  uint16_t* scales;
+  uint16_t* zeros;
+  int64_t N;
+  int64_t K;
+  int64_t stride_wn;
+  int64_t stride_wk;
+  int32_t group_size;
+  int32_t reserved;
+} w4_quantize_problem;
+
+/*
+ * Up to W4_MAX_GROUPED weights quantized as by w4_quantize (same outputs,
+ * bit for bit), all of dtype w_dtype: ONE kernel launch when every weight has
+ * dense 16-byte-aligned rows and all share one group size <= 512 (the
+ * weights of a decoder block), else one w4_quantize per weight, in order.
+ * No single counterpart in the reference: it fuses the per-linear
+ * quantize_int4 calls that quantize_model_linears issues for the linears of
+ * one block (int4_triton/qlinear.py:55-68, quantize.py:67-96).
+ */
+int w4_quantize_grouped(const w4_quantize_problem* problems, int count, int w_dtype, void* stream);
+
+/*
  * W_hat[N, K] (dense, row-major) = round_once_to_out_dtype((q - z) * s),
  * computed exactly in fp32.  out_dtype: W4_DTYPE_BF16/FP16/FP32.
  * Replaces: int4_triton/quantize.py:128-135 (dequantize_int4_ref) as used by

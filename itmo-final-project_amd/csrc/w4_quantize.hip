@@ -210,11 +210,31 @@ constexpr int quantize_waves_per_tile(int G) { return G / 8 < QSWAVES ? G / 8 : 
 
 // Single-pass kernel for G <= 512: lanes_per_row = G/8 lanes each own one
 // packed word of a row; 64/lanes_per_row rows are processed per iteration.
+// One weight of a quantize launch (w4_quantize_grouped puts several in one).
+struct QuantArgs {
+  const uint16_t* w;
+  int32_t* qw;
+  uint16_t* sc;
+  uint16_t* ze;
+  int64_t N, K, swn, swk;
+  int64_t tiles_n, tiles_total;
+};
+
+constexpr int kQuantMaxGrouped = 8;
+struct QuantGroupedArgs {
+  QuantArgs prob[kQuantMaxGrouped];
+  int wg_start[kQuantMaxGrouped + 1];
+  int count;
+};
+
+// The tiles of workgroup `blk` of one weight (see quantize_small_group_kernel).
 template <int DT, int G, bool VEC>
-__global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
-    const uint16_t* __restrict__ w, int64_t N, int64_t K, int64_t swn, int64_t swk,
-    int32_t* __restrict__ qw, uint16_t* __restrict__ sc, uint16_t* __restrict__ ze,
-    int64_t tiles_n, int64_t tiles_total) {
+__device__ __forceinline__ void quantize_small_group_tiles(const QuantArgs& qa, int blk) {
+  const uint16_t* __restrict__ w = qa.w;
+  int32_t* __restrict__ qw = qa.qw;
+  uint16_t* __restrict__ sc = qa.sc;
+  uint16_t* __restrict__ ze = qa.ze;
+  const int64_t N = qa.N, K = qa.K, swn = qa.swn, swk = qa.swk, tiles_n = qa.tiles_n, tiles_total = qa.tiles_total;
   constexpr int L = G / 8;            // lanes per row (1..64)
   constexpr int RPI = 64 / L;         // rows per iteration
   constexpr int WPT = quantize_waves_per_tile(G);
@@ -229,7 +249,7 @@ __global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: tile math stays scalar
   const int ts = wv / WPT, sub = wv % WPT;  // tile slot, row slice of this wave
   // the host keeps tile counts below 2^31, so the tile index math is 32-bit
-  const int t = (int)blockIdx.x * TPB + ts;
+  const int t = blk * TPB + ts;
   const bool active = t < (int)tiles_total;
   const int g = active ? t / (int)tiles_n : 0;
   const int64_t n0 = active ? (int64_t)(t - g * (int)tiles_n) * QROWS : 0;
@@ -314,6 +334,23 @@ __global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(
       }
     }
   }
+}
+
+template <int DT, int G, bool VEC>
+__global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_kernel(QuantArgs qa) {
+  quantize_small_group_tiles<DT, G, VEC>(qa, (int)blockIdx.x);
+}
+
+// Several weights in one launch: workgroup b belongs to the weight whose
+// workgroup range holds it (the ranges follow each other in order).
+template <int DT, int G>
+__global__ __launch_bounds__(QSWAVES * 64) void quantize_small_group_grouped_kernel(QuantGroupedArgs ga) {
+  const int b = blockIdx.x;
+  int p = 0;
+#pragma unroll
+  for (int i = 1; i < kQuantMaxGrouped; ++i)
+    if (i < ga.count && b >= ga.wg_start[i]) p = i;
+  quantize_small_group_tiles<DT, G, true>(ga.prob[p], b - ga.wg_start[p]);
 }
 
 // Two-pass kernel for G > 512 (per-channel G = K included): pass 1 reduces
@@ -471,10 +508,10 @@ static void launch_quantize(const uint16_t* w, int64_t N, int64_t K, int64_t swn
   const int64_t tpb = small ? w4::QSWAVES / w4::quantize_waves_per_tile(G) : w4::QWAVES;
   const dim3 grid((unsigned)((tiles_total + tpb - 1) / tpb));
   const dim3 block((small ? w4::QSWAVES : w4::QWAVES) * 64);
-#define W4_QS(GG)                                                                         \
-  case GG:                                                                                \
-    hipLaunchKernelGGL((w4::quantize_small_group_kernel<DT, GG, VEC>), grid, block, 0, st, \
-                       w, N, K, swn, swk, qw, sc, ze, tiles_n, tiles_total);              \
+  const w4::QuantArgs qa{w, qw, sc, ze, N, K, swn, swk, tiles_n, tiles_total};
+#define W4_QS(GG)                                                                                  \
+  case GG:                                                                                         \
+    hipLaunchKernelGGL((w4::quantize_small_group_kernel<DT, GG, VEC>), grid, block, 0, st, qa); \
     return;
   switch (G) {
     W4_QS(8)
@@ -523,6 +560,71 @@ extern "C" int w4_quantize(const void* w, int w_dtype, int64_t N, int64_t K, int
     else launch_quantize<W4_DTYPE_FP16, false>(wp, N, K, stride_wn, stride_wk, (int)G, qweight, scales, zeros, st);
   }
   return check_launch("w4_quantize");
+}
+
+// One grouped launch when every weight takes the single-pass 128-bit path
+// with the same group size; otherwise one w4_quantize per weight, in order.
+extern "C" int w4_quantize_grouped(const w4_quantize_problem* problems, int count, int w_dtype, void* stream) {
+  clear_error();
+  if (count < 1 || count > W4_MAX_GROUPED)
+    return fail(W4_ERR_INVALID, "w4_quantize_grouped: count must be in [1, %d]", W4_MAX_GROUPED);
+  if (!problems) return fail(W4_ERR_INVALID, "w4_quantize_grouped: null problem list");
+  if (w_dtype != W4_DTYPE_BF16 && w_dtype != W4_DTYPE_FP16)
+    return fail(W4_ERR_INVALID, "w4_quantize_grouped: weight dtype must be bf16 or fp16 (got code %d)", w_dtype);
+  static_assert(W4_MAX_GROUPED <= w4::kQuantMaxGrouped, "grouped quantize capacity");
+  w4::QuantGroupedArgs ga{};
+  int64_t G0 = -1, wgs = 0;
+  bool one_launch = true;
+  for (int i = 0; i < count; ++i) {
+    const w4_quantize_problem& q = problems[i];
+    if (q.N < 0 || q.K <= 0)
+      return fail(W4_ERR_INVALID, "w4_quantize_grouped: bad shape in problem %d (N=%lld K=%lld)", i,
+                  (long long)q.N, (long long)q.K);
+    const int64_t G = q.group_size == -1 ? q.K : q.group_size;
+    if (G <= 0 || q.K % G != 0 || G % 8 != 0 || !is_pow2(G))
+      return fail(W4_ERR_INVALID, "w4_quantize_grouped: bad group size %d in problem %d (K=%lld)", q.group_size, i,
+                  (long long)q.K);
+    if (q.N > 0 && (!q.w || !q.qweight || !q.scales || !q.zeros))
+      return fail(W4_ERR_INVALID, "w4_quantize_grouped: null pointer in problem %d", i);
+    const bool vec = q.stride_wk == 1 && (q.stride_wn % 8) == 0 && ((uintptr_t)q.w % 16) == 0 &&
+                     ((q.N - 1) * q.stride_wn + q.K) * 2 < (1LL << 31) && ((q.N + 63) / 64) * (q.K / G) < (1LL << 30);
+    one_launch = one_launch && q.N > 0 && vec && G <= 512 && (G0 < 0 || G == G0);
+    G0 = G;
+    if (!one_launch) continue;
+    const int64_t tiles_n = (q.N + w4::QROWS - 1) / w4::QROWS, tiles_total = tiles_n * (q.K / G);
+    const int64_t tpb = w4::QSWAVES / w4::quantize_waves_per_tile((int)G);
+    ga.prob[i] = w4::QuantArgs{static_cast<const uint16_t*>(q.w), q.qweight, q.scales, q.zeros, q.N, q.K,
+                               q.stride_wn, q.stride_wk, tiles_n, tiles_total};
+    ga.wg_start[i] = (int)wgs;
+    wgs += (tiles_total + tpb - 1) / tpb;
+    one_launch = wgs < (1LL << 30);
+  }
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!one_launch) {
+    for (int i = 0; i < count; ++i) {
+      const w4_quantize_problem& q = problems[i];
+      const int rc = w4_quantize(q.w, w_dtype, q.N, q.K, q.stride_wn, q.stride_wk, q.group_size, q.qweight,
+                                 q.scales, q.zeros, stream);
+      if (rc != W4_OK) return rc;
+    }
+    return W4_OK;
+  }
+  for (int i = count; i <= w4::kQuantMaxGrouped; ++i) ga.wg_start[i] = (int)wgs;
+  ga.count = count;
+  const dim3 grid((unsigned)wgs), block(w4::QSWAVES * 64);
+#define W4_QG(DT, GG)                                                                                \
+  case GG:                                                                                           \
+    hipLaunchKernelGGL((w4::quantize_small_group_grouped_kernel<DT, GG>), grid, block, 0, st, ga); \
+    break;
+  if (w_dtype == W4_DTYPE_BF16) {
+    switch (G0) { W4_QG(W4_DTYPE_BF16, 8) W4_QG(W4_DTYPE_BF16, 16) W4_QG(W4_DTYPE_BF16, 32) W4_QG(W4_DTYPE_BF16, 64)
+                  W4_QG(W4_DTYPE_BF16, 128) W4_QG(W4_DTYPE_BF16, 256) W4_QG(W4_DTYPE_BF16, 512) default: break; }
+  } else {
+    switch (G0) { W4_QG(W4_DTYPE_FP16, 8) W4_QG(W4_DTYPE_FP16, 16) W4_QG(W4_DTYPE_FP16, 32) W4_QG(W4_DTYPE_FP16, 64)
+                  W4_QG(W4_DTYPE_FP16, 128) W4_QG(W4_DTYPE_FP16, 256) W4_QG(W4_DTYPE_FP16, 512) default: break; }
+  }
+#undef W4_QG
+  return check_launch("w4_quantize_grouped");
 }
 
 extern "C" int w4_dequantize(const int32_t* qweight, const uint16_t* scales, const uint16_t* zeros,

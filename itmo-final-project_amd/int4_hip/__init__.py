@@ -7,7 +7,8 @@ hold), running hand-written gfx950 HIP kernels through the C-ABI library
 ``libint4_hip.so``.
 """
 from . import quantize  # callable: quantize(w, group_size) == quantize_int4(w, group_size)
-from .quantize import dequantize_int4, dequantize_int4_ref, quantize_int4, quantize_int4_ref, unpack_int4_ref
+from .quantize import (dequantize_int4, dequantize_int4_ref, quantize_int4, quantize_int4_grouped,
+                       quantize_int4_ref, unpack_int4_ref)
 from .gemm import w4a16_matmul, w4a16_matmul_grouped, w16a16_matmul
 from .qlinear import Int4Linear, quantize_model_linears
 
@@ -24,4 +25,5 @@ __all__ = [
     "dequantize_int4",
     "unpack_int4_ref",
     "w4a16_matmul_grouped",
+    "quantize_int4_grouped",
 ]

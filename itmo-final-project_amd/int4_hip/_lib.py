@@ -48,11 +48,29 @@ class Problem(ctypes.Structure):
     ]
 
 
+class QuantProblem(ctypes.Structure):
+    """Mirror of ``w4_quantize_problem`` (include/int4_hip.h)."""
+
+    _fields_ = [
+        ("w", _c_vp),
+        ("qweight", _c_vp),
+        ("scales", _c_vp),
+        ("zeros", _c_vp),
+        ("N", _c_i64),
+        ("K", _c_i64),
+        ("stride_wn", _c_i64),
+        ("stride_wk", _c_i64),
+        ("group_size", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
 # symbol -> (restype, argtypes); exactly the functions include/int4_hip.h declares
 SIGNATURES = {
     "w4_abi_version": (_c_int, []),
     "w4_last_error": (ctypes.c_char_p, []),
     "w4_quantize": (_c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_vp, _c_vp, _c_vp, _c_vp]),
+    "w4_quantize_grouped": (_c_int, [ctypes.POINTER(QuantProblem), _c_int, _c_int, _c_vp]),
     "w4_dequantize": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_vp]),
     "w4a16_workspace_bytes": (_c_sz, [_c_i64, _c_i64, _c_i64, _c_int]),
     "w4a16_gemm": (_c_int, [_c_vp, _c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp, _c_vp, _c_int,

@@ -76,6 +76,39 @@ def quantize_int4(w: torch.Tensor, group_size: int = 128):
     return qweight, scales, zeros
 
 
+def quantize_int4_grouped(ws, group_size: int = 128):
+    """Quantize several weights W_i[N_i, K_i] (one dtype, on one GPU) as
+    ``quantize_int4`` does, bit for bit, in one kernel launch when every
+    weight has dense 16-byte-aligned rows (and the group size is <= 512);
+    else one launch per weight.  Returns a list of ``(qweight, scales,
+    zeros)`` triples.  No single counterpart in the reference: it fuses the
+    per-linear ``quantize_int4`` calls of one block
+    (int4_triton/qlinear.py:55-68)."""
+    ws = list(ws)
+    assert 1 <= len(ws) <= _lib.MAX_GROUPED
+    dt, dev = ws[0].dtype, ws[0].device
+    assert dt in (torch.float16, torch.bfloat16)
+    probs = (_lib.QuantProblem * len(ws))()
+    outs = []
+    for i, w in enumerate(ws):
+        assert w.dim() == 2 and w.is_cuda and w.dtype == dt and w.device == dev
+        N, K = w.shape
+        G = _resolve_group(K, group_size)
+        assert K % G == 0 and G % 8 == 0
+        assert G > 0 and (G & (G - 1)) == 0, "group_size must be a power of 2"
+        qweight = torch.empty((K // 8, N), dtype=torch.int32, device=dev)
+        scales = torch.empty((K // G, N), dtype=torch.float16, device=dev)
+        zeros = torch.empty_like(scales)
+        probs[i] = _lib.QuantProblem(w.data_ptr(), qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(), N, K,
+                                     w.stride(0), w.stride(1), group_size, 0)
+        outs.append((qweight, scales, zeros))
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.w4_quantize_grouped(probs, len(ws), _DT[dt], _stream_ptr(dev))
+    _lib.check(rc, "w4_quantize_grouped")
+    return outs
+
+
 def dequantize_int4(qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
                     dtype=torch.float16) -> torch.Tensor:
     """W_hat[N, K] = one rounding to ``dtype`` of the exact fp32 (q - z) * s, on the GPU.

@@ -180,3 +180,57 @@ def test_quantize_degenerate_groups_every_width(dt, g):
     np.testing.assert_array_equal(qw, rq)
     np.testing.assert_array_equal(s, rs)
     np.testing.assert_array_equal(z, rz)
+
+
+# grouped quantize (one launch for the weights of a block): every output bit
+# equal to the lone kernel's, on the block's shapes and on the routes that fall
+# back to one launch per weight (mixed group sizes, strided rows, G = K)
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("G", [32, 128, 512])
+def test_quantize_grouped_matches_lone(dt, G):
+    shapes = [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192),
+              (100, 1024)]
+    print(f"[quantize grouped] G={G} {dt}", flush=True)
+    ws = [randn((N, K), seed=900 + i, sigma=0.02, dtype=dt).to(DEV) for i, (N, K) in enumerate(shapes)]
+    ws[-1][3, 5] = float("nan")  # a NaN group takes the exact path in both
+    grouped = int4_hip.quantize_int4_grouped(ws, G)
+    for w, (gq, gs, gz) in zip(ws, grouped):
+        q, s, z = int4_hip.quantize_int4(w, G)
+        assert torch.equal(gq, q)
+        assert torch.equal(gs.view(torch.int16), s.view(torch.int16))
+        assert torch.equal(gz.view(torch.int16), z.view(torch.int16))
+
+
+@pytest.mark.parametrize("case", ["mixed_groups", "strided", "per_channel"])
+def test_quantize_grouped_fallbacks(case):
+    print(f"[quantize grouped fallback] {case}", flush=True)
+    ws = [randn((300, 1024), seed=950 + i, sigma=0.02).to(DEV) for i in range(3)]
+    if case == "strided":
+        ws[1] = randn((300, 2048), seed=960, sigma=0.02).to(DEV)[:, ::2]
+    gsz = -1 if case == "per_channel" else 128
+    outs = int4_hip.quantize_int4_grouped(ws, gsz)
+    if case == "mixed_groups":  # the Python API takes one group size; the C-ABI takes one per weight
+        outs = None
+    for w, o in zip(ws, outs or []):
+        q, s, z = int4_hip.quantize_int4(w, gsz)
+        assert torch.equal(o[0], q) and torch.equal(o[1].view(torch.int16), s.view(torch.int16))
+        assert torch.equal(o[2].view(torch.int16), z.view(torch.int16))
+    if case == "mixed_groups":
+        from int4_hip import _lib
+        lib = _lib.load()
+        gs = [32, 128, 64]
+        probs = (_lib.QuantProblem * 3)()
+        outs = []
+        for i, (w, g) in enumerate(zip(ws, gs)):
+            N, K = w.shape
+            o = (torch.empty((K // 8, N), dtype=torch.int32, device=DEV),
+                 torch.empty((K // g, N), dtype=torch.float16, device=DEV),
+                 torch.empty((K // g, N), dtype=torch.float16, device=DEV))
+            probs[i] = _lib.QuantProblem(w.data_ptr(), o[0].data_ptr(), o[1].data_ptr(), o[2].data_ptr(), N, K,
+                                         w.stride(0), w.stride(1), g, 0)
+            outs.append(o)
+        _lib.check(lib.w4_quantize_grouped(probs, 3, _lib.DTYPE_BF16, torch.cuda.current_stream().cuda_stream),
+                   "w4_quantize_grouped")
+        for w, g, o in zip(ws, gs, outs):
+            q, s, z = int4_hip.quantize_int4(w, g)
+            assert torch.equal(o[0], q) and torch.equal(o[1].view(torch.int16), s.view(torch.int16))
