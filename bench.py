@@ -495,6 +495,63 @@ def summarize_prefill_prof(d: Path) -> str:
     return "\n".join(head + ["", "Per linear:", ""] + lines + ["", "Fused block (4 calls):", ""] + fused)
 
 
+def summarize_grid(d: Path, match: str = "") -> str:
+    """Markdown table of a rocprofv3 run directory (``trace/``, ``fetch/``,
+    ``write/``, optional ``sq/``) per (kernel, workgroup count): average
+    duration, FETCH_SIZE / WRITE_SIZE per dispatch scaled by the same counters
+    on the run's 32 MiB device copy (``--copy-calib``), and the other
+    counters per dispatch.  ``match``: keep kernels whose name contains it."""
+    import csv
+    import gzip
+
+    def rows(sub, name):
+        fs = sorted((d / sub).glob(f"**/run_{name}.csv*"))
+        if not fs:
+            return []
+        f = fs[0]
+        with (gzip.open(f, "rt") if f.suffix == ".gz" else open(f)) as fh:
+            return list(csv.DictReader(fh))
+
+    def short(n):
+        return n.replace("void ", "").split("(")[0]
+
+    dur = {}
+    for r in rows("trace", "kernel_trace"):
+        if "w4::" in r["Kernel_Name"] and match in r["Kernel_Name"]:
+            key = (short(r["Kernel_Name"]), int(r["Grid_Size_X"]) // int(r["Workgroup_Size_X"]))
+            dur.setdefault(key, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    calib, ctr = {}, {}
+    for sub in ("fetch", "write", "sq"):
+        per = {}
+        for r in rows(sub, "counter_collection"):
+            k = (r["Dispatch_Id"], r["Kernel_Name"], int(r["Grid_Size"]) // int(r["Workgroup_Size"]))
+            c = per.setdefault(k, {})
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        for (_, kn, wg), cs in sorted(per.items(), key=lambda kv: int(kv[0][0])):
+            if "copyBuffer" in kn:
+                for cname, v in cs.items():
+                    calib.setdefault(cname, 32768.0 / v)
+            elif "w4::" in kn and match in kn:
+                for cname, v in cs.items():
+                    ctr.setdefault((short(kn), wg), {}).setdefault(cname, []).append(v)
+    fs, ws = calib.get("FETCH_SIZE"), calib.get("WRITE_SIZE")
+    out = [f"- calibration (32 MiB device copy): FETCH_SIZE x {fs or 0:.3f}, WRITE_SIZE x {ws or 0:.3f}", "",
+           "| kernel | WGs | dispatches | avg us | FETCH MB | WRITE MB | other counters per dispatch |",
+           "|---|---|---|---|---|---|---|"]
+    for key in sorted(dur):
+        c = ctr.get(key, {})
+
+        def mb(name, scale):
+            v = c.get(name)
+            return "-" if not v or not scale else f"{sum(v) / len(v) * scale * 1024 / 1e6:.2f}"
+        other = ", ".join(f"{n} {sum(v) / len(v):.4g}" for n, v in sorted(c.items())
+                          if n not in ("FETCH_SIZE", "WRITE_SIZE"))
+        t = dur[key]
+        out.append(f"| `{key[0]}` | {key[1]} | {len(t)} | {sum(t) / len(t):.2f} | {mb('FETCH_SIZE', fs)} | "
+                   f"{mb('WRITE_SIZE', ws)} | {other} |")
+    return "\n".join(out)
+
+
 def profiled_traffic() -> dict | None:
     """HBM bytes per launch of the roofline kernel, from the committed profile."""
     if not PROFILE.exists():
@@ -502,6 +559,26 @@ def profiled_traffic() -> dict | None:
     for line in PROFILE.read_text().splitlines():
         if line.startswith("- traffic_bytes_per_launch:"):
             return {"bytes": int(float(line.split(":")[1])), "source": str(PROFILE.relative_to(ROOT))}
+    return None
+
+
+PREFILL_PROFILE = ROOT / "profiles" / "prefill_per_linear_m128_m512_m2048.md"
+MFMA_ROOFLINE_LINEAR = "gate"  # M = 2048: gate/up (one kernel, two launches) take the largest share
+
+
+def profiled_prefill(M: int, linear: str) -> dict | None:
+    """Main kernel and HBM bytes per call of one linear of the prefill
+    section, from the committed per-linear profile table."""
+    if not PREFILL_PROFILE.exists():
+        return None
+    for line in PREFILL_PROFILE.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 9 and cells[0] == str(M) and cells[1] == linear:
+            try:
+                traffic = int(float(cells[7]) * 1e6)
+            except ValueError:
+                traffic = None
+            return {"kernel": cells[2].strip("`"), "bytes": traffic, "source": str(PREFILL_PROFILE.relative_to(ROOT))}
     return None
 
 
@@ -526,9 +603,16 @@ def main() -> int:
                     help="print the profile summary of a rocprofv3 run directory and exit (no GPU use)")
     ap.add_argument("--summarize-prefill-prof", default=None, metavar="DIR",
                     help="print the per-linear tables of a rocprofv3 run of --only prefill and exit (no GPU use)")
+    ap.add_argument("--summarize-grid", metavar="DIR",
+                    help="print per (kernel, workgroup count) times and counters of a rocprofv3 run directory "
+                         "and exit (no GPU use)")
+    ap.add_argument("--match", default="", help="with --summarize-grid: kernels whose name contains this")
     args = ap.parse_args()
     if args.summarize_prof:
         print(summarize_prof(Path(args.summarize_prof)))
+        return 0
+    if args.summarize_grid:
+        print(summarize_grid(Path(args.summarize_grid), args.match))
         return 0
     if args.summarize_prefill_prof:
         print(summarize_prefill_prof(Path(args.summarize_prefill_prof)))
@@ -861,6 +945,24 @@ def main() -> int:
     read_ceiling = hbm_read_ceiling(dev, stream, bytes1, nsets) if "decode" in only else None
 
     traffic = profiled_traffic()
+    # the M = 2048 half of the metric: the dominant prefill kernel against the
+    # bf16 MFMA peak (its per-call time from the section's graph of 4 lone
+    # calls, timed with events on the launch stream; its traffic from the
+    # committed per-linear profile)
+    pre_roof = None
+    if pre:
+        name = MFMA_ROOFLINE_LINEAR + "_proj"
+        _, N, K = next(lin for lin in LINEARS if lin[0] == name)
+        t_us = pre[2048]["per_linear_us"][name]
+        ach = 2 * 2048 * N * K / (t_us * 1e-6) / 1e12
+        prof = profiled_prefill(2048, MFMA_ROOFLINE_LINEAR)
+        pre_roof = {"bound": "mfma", "linear": name, "M": 2048,
+                    "kernel": ("w4::" + prof["kernel"].replace("w4::", "")) if prof else None,
+                    "kernel_us": t_us, "achieved": round(ach, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": round(ach / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "traffic": prof["bytes"] if prof else None, "traffic_source": prof["source"] if prof else None,
+                    "algorithmic_bytes": lin_bytes(N, K, 2048),
+                    "kernel_time_source": "hip-events-on-launch-stream over 10 graph replays of 4 lone calls"}
     out = {
         "metric": METRIC,
         "value": round(value, 2) if value is not None else None,
@@ -904,6 +1006,7 @@ def main() -> int:
         "prefill": {str(k): v for k, v in pre.items()},
         "prefill_m2048_tflops": pre[2048]["tflops"] if pre else None,
         "prefill_m2048_mfma_frac": round(pre[2048]["tflops"] / MFMA_BF16_PEAK_TFLOPS, 4) if pre else None,
+        "prefill_m2048_roofline": pre_roof,
         "quantize_us_per_block": round(q_ms * 1e3, 2) if q_ms else None,
         "quantize_gbps": round(q_bytes / (q_ms * 1e-3) / 1e9, 1) if q_ms else None,
         "quantize_7_launches_us_per_block": round(q7_ms * 1e3, 2) if q7_ms else None,
