@@ -256,6 +256,34 @@ SIDE = [  # M, N, K, G, layout
 ]
 
 
+# the sixteen-row slice kernel: a partial last slice, K split into 2 / 4 / 8
+# parts (finished by the last part to arrive), every group class, column
+# tiles not a multiple of 8 (the tail of the XCD-ordered workgroup blocks),
+# lone and grouped, repeated calls
+SLICES = [  # M, N, K, G
+    (17, 520, 4096, 32), (33, 96, 8192, 64), (40, 2048, 6144, 128), (63, 72, 16384, 256),
+    (100, 4096, 2048, 128), (128, 200, 8192, 512), (9, 8, 12288, 64), (120, 1000, 4096, 32),
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("M,N,K,G", SLICES)
+def test_exact_row_slices(M, N, K, G, dt):
+    _bound_ok(K)
+    print(f"[exact slices] M={M} N={N} K={K} G={G} {dt}", flush=True)
+    qw, s, z = _to_dev_weights(N, K, G, seed=8000 + N + K + G)
+    xn = _exact_x_np(M, K, seed=8100 + M)
+    x = _to_dev_x(xn, dt)
+    y = _exact_y(M, N, K, G, 8000 + N + K + G, 8100 + M)
+    for _ in range(2):
+        _assert_bits(int4_hip.w4a16_matmul(x, qw, s, z), y, dt, f"slices lone M={M} N={N} K={K} G={G}")
+    other = _to_dev_weights(512, 2048, G, seed=8200)
+    xo = _to_dev_x(_exact_x_np(M, 2048, seed=8300 + M), dt)
+    outs = int4_hip.w4a16_matmul_grouped([x, xo], [(qw, s, z), other])
+    _assert_bits(outs[0], y, dt, f"slices grouped M={M} N={N} K={K} G={G}")
+    _assert_bits(outs[1], _exact_y(M, 512, 2048, G, 8200, 8300 + M), dt, f"slices grouped partner M={M}")
+
+
 @pytest.mark.parametrize("dt", ["bf16", "fp16"])
 @pytest.mark.parametrize("M,N,K,G,layout", SIDE)
 def test_exact_side_routes(M, N, K, G, layout, dt):
