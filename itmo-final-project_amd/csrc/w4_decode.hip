@@ -654,9 +654,10 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   const int per_wave = ((S + WV - 1) / WV + NL - 1) / NL * NL;
   const int wb = s0 + min(S, wv * per_wave);
   const int we = s0 + min(S, min(S, wv * per_wave) + per_wave);
-  // Row slices (problems of more than 16 rows): the workgroup computes its
-  // column tile (or K part) for rows [16 sl0, 16 sl0 + 16) of the problem.
-  auto rows_of = [&](int sl) { return MR == 1 ? 1 : MR == 16 ? min(16, a.M - 16 * sl) : a.M; };
+  // Row slices (sixteen-row kernel, problems of more than 16 rows): the
+  // workgroup computes its column tile (or K part) for rows [16 sl0,
+  // 16 sl0 + M) of the problem.
+  const int M = MR == 1 ? 1 : MR == 16 ? min(16, a.M - 16 * sl0) : a.M;
 
   const __amdgpu_buffer_rsrc_t rq =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, kDecBufFlags);
@@ -664,29 +665,22 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       __builtin_amdgcn_make_buffer_rsrc((void*)a.sc, (short)0, (int)a.sz_bytes, kDecBufFlags);
   const __amdgpu_buffer_rsrc_t rz =
       __builtin_amdgcn_make_buffer_rsrc((void*)a.ze, (short)0, (int)a.sz_bytes, kDecBufFlags);
-  // activations of slice sl: rows [16 sl, 16 sl + rows_of(sl)) (one slice: the
-  // problem's range)
-  auto x_rsrc = [&](int sl) {
-    if (MR < 16 || a.slices == 1)
-      return __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, kDecBufFlags);
-    const int64_t r0 = 16 * (int64_t)sl;
-    const int xb = (int)(((int64_t)(rows_of(sl) - 1) * a.sxm + K) * 2);
-    return __builtin_amdgcn_make_buffer_rsrc((void*)(a.x + r0 * a.sxm), (short)0, xb, kDecBufFlags);
-  };
+  // activations of the slice's rows (one slice: the problem's range)
+  const bool sliced = MR == 16 && a.slices > 1;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(sliced ? a.x + (int64_t)16 * sl0 * a.sxm : a.x), (short)0,
+      sliced ? (int)(((int64_t)(M - 1) * a.sxm + K) * 2) : (int)a.x_bytes, kDecBufFlags);
 
   const uint32_t step_bytes = (uint32_t)RPS * 4u * (uint32_t)N;
   const uint32_t w_lane = ((uint32_t)lr * (uint32_t)N + (uint32_t)(n0 + 4 * lq)) * 4u;
   // activation entry f = 64 j + lane of a round: row f / XE, entry f % XE
-  // (k8 row sb * RPS + f % XE); entries of rows past the slice's rows read zeros
+  // (k8 row sb * RPS + f % XE); entries of rows past M read zeros
   uint32_t x_lane[XLD];
-  auto set_x_lanes = [&](int rows) {
 #pragma unroll
-    for (int j = 0; j < XLD; ++j) {
-      const int f = 64 * j + lane, m = f / XE, e = f % XE;
-      x_lane[j] = (f < MR * XE && m < rows) ? ((uint32_t)m * (uint32_t)a.sxm + (uint32_t)e * 8u) * 2u : kDecOOB;
-    }
-  };
-  set_x_lanes(rows_of(sl0));
+  for (int j = 0; j < XLD; ++j) {
+    const int f = 64 * j + lane, m = f / XE, e = f % XE;
+    x_lane[j] = (f < MR * XE && m < M) ? ((uint32_t)m * (uint32_t)a.sxm + (uint32_t)e * 8u) * 2u : kDecOOB;
+  }
   const uint32_t sz_oob = lane < NP * LPG ? 0u : kDecOOB;
   const uint32_t sz_lane = (uint32_t)(lane / LPG) * (uint32_t)N * 2u + (uint32_t)(n0 * 2 + (lane % LPG) * 16);
   uint8_t* x_lds = lds + wv * WLDS;
@@ -715,17 +709,13 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     u32x4 w[NL];
     u32x4 x[XLD], s, z;
   };
-  auto load_x = [&](Round& r, __amdgpu_buffer_rsrc_t rx, int sb) {
-    const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
-#pragma unroll
-    for (int j = 0; j < XLD; ++j)
-      r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (x_lane[j] + (uint32_t)sb * RPS * 16u) | oob, 0, 0);
-  };
   // Issue order = order of use: activations, scales, zeros, weights.
   auto load_round = [&](Round& r, int sb) {
     const uint32_t oob = sb < we ? 0u : kDecOOB;  // scalar
     __builtin_amdgcn_sched_barrier(0);
-    load_x(r, x_rsrc(sl0), sb);
+#pragma unroll
+    for (int j = 0; j < XLD; ++j)
+      r.x[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, (x_lane[j] + (uint32_t)sb * RPS * 16u) | oob, 0, 0);
     const uint32_t g0 = (uint32_t)((sb * SK) >> a.gshift);
     const uint32_t so = (g0 * (uint32_t)N * 2u + sz_lane) | sz_oob | oob;
     r.s = __builtin_amdgcn_raw_buffer_load_b128(rs, so, 0, kDecWeightAux);
@@ -742,18 +732,16 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   f32x4 xs;
   float tot[4][RE];
 
-  // stage the round's activations (permuted) and, with_sz, its scales and zeros
-  auto stage_round = [&](const Round& r, bool with_sz) {
+  // stage the round's activations (permuted), scales and zeros
+  auto stage_round = [&](const Round& r) {
 #pragma unroll
     for (int j = 0; j < XLD; ++j) {
       const int f = 64 * j + lane, m = f / XE, e = f % XE;
       if (f < MR * XE)
         *reinterpret_cast<u32x4*>(x_lds + xpos(m, (e / RPS) * SLOTS + e % RPS)) = dec_perm_x(r.x[j]);
     }
-    if (with_sz) {
-      *reinterpret_cast<u32x4*>(s_lds + lane * 16) = r.s;
-      *reinterpret_cast<u32x4*>(z_lds + lane * 16) = r.z;
-    }
+    *reinterpret_cast<u32x4*>(s_lds + lane * 16) = r.s;
+    *reinterpret_cast<u32x4*>(z_lds + lane * 16) = r.z;
     __builtin_amdgcn_wave_barrier();
   };
   auto compute_round = [&](const Round& r, int sb) {
@@ -802,10 +790,11 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
   constexpr int RROW = MR == 16 ? 64 : 128;
   float* red = reinterpret_cast<float*>(lds + (MR >= 8 ? 0 : one_red_offset(MR)));
 
-  // Reduce the workgroup's partials of slice sl and store them (or, K split
-  // with several rows, publish them; the last part to arrive stores the sum).
-  auto finish_slice = [&](int sl) {
-    const int M = rows_of(sl);
+  // Reduce the workgroup's partials and store them (or, K split, publish
+  // them; the last part to arrive stores the sum).  Slice sl0 has its own
+  // rows of y, arrival counters and partial tiles.
+  const int sl = sl0;
+  auto finish = [&]() {
     uint16_t* const y = a.y + (int64_t)(16 * sl) * a.ldy;
     if (owner) {
       // the four columns of an output quad as one 16-byte store per row
@@ -963,26 +952,26 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
     if (wb < we) {
       Round r;
       load_round(r, wb);
-      stage_round(r, true);
+      stage_round(r);
       compute_round(r, wb);
     }
-    finish_slice(sl0);
+    finish();
   } else {
     clear_tot();
     Round ra, rb;
     load_round(ra, wb);
     load_round(rb, wb + NL);
     for (int sb = wb; sb < we; sb += 2 * NL) {
-      stage_round(ra, true);
+      stage_round(ra);
       compute_round(ra, sb);
       load_round(ra, sb + 2 * NL);
       if (sb + NL < we) {
-        stage_round(rb, true);
+        stage_round(rb);
         compute_round(rb, sb + NL);
       }
       load_round(rb, sb + 3 * NL);
     }
-    finish_slice(0);
+    finish();
   }
 }
 
