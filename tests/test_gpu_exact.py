@@ -253,6 +253,7 @@ SIDE = [  # M, N, K, G, layout
     (64, 300, 4096, 8, "dense"), (65, 96, 520, 8, "dense"), (130, 73, 512, 64, "dense"),
     (200, 300, 512, 64, "strided"), (512, 2048, 2048, 16, "dense"), (777, 1000, 1024, 32, "strided"),
     (2048, 96, 520, 8, "dense"), (300, 8192, 2048, 128, "offset"),
+    (33, 73, 2048, 64, "dense"), (100, 300 + 2, 1024, 128, "dense"),  # generic decode kernel in 16-row slices
 ]
 
 
