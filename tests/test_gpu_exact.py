@@ -254,6 +254,7 @@ SIDE = [  # M, N, K, G, layout
     (200, 300, 512, 64, "strided"), (512, 2048, 2048, 16, "dense"), (777, 1000, 1024, 32, "strided"),
     (2048, 96, 520, 8, "dense"), (300, 8192, 2048, 128, "offset"),
     (33, 73, 2048, 64, "dense"), (100, 300 + 2, 1024, 128, "dense"),  # generic decode kernel in 16-row slices
+    (700, 1000, 1024, 64, "dense"), (2048, 520, 2048, 128, "dense"),  # pf3 with a partial last column tile
 ]
 
 
