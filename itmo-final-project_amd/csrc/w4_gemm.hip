@@ -28,6 +28,10 @@ int w4_prefill_fast_launch(const void* x, int x_dtype, int64_t M, int64_t N, int
                            int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
                            void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
 
+int w4_rows_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int x_dtype,
+                   int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes, hipStream_t st);
+size_t w4_rows_workspace_bytes(const w4a16_problem* problems, const int64_t* sxm, int count, int64_t M);
+
 // Reference regime boundary: M <= SMALL_M = 64 uses split-K (gemm.py:17, 265).
 int w4_prefill_grouped_launch(const w4a16_problem* problems, int count, int x_dtype, int64_t M, hipStream_t st);
 
@@ -209,6 +213,10 @@ extern "C" size_t w4a16_grouped_workspace_bytes(const w4a16_problem* problems, i
       for (int i = 0; i < count; ++i) sxm[i] = problems[i].K, mr[i] = M;
       const size_t d = w4_decode_workspace_bytes(problems, sxm, count, kDecodeM, mr);
       most = d > most ? d : most;
+      if (M <= kSmallM) {
+        const size_t r = w4_rows_workspace_bytes(problems, sxm, count, M);
+        most = r > most ? r : most;
+      }
     }
     return most;
   }
@@ -230,7 +238,9 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
   const int rc = check_grouped(problems, count, M);
   if (rc != W4_OK) return rc;
   if (M > kDecodeM) {
-    // up to 64 rows, one decode launch with every problem in 16-row slices;
+    // up to 64 rows, one decode launch with every problem in 16-row slices
+    // (49..64 rows: the several-row kernel where every problem fits it; up to
+    // 128 rows when every N <= 4096);
     // else one launch when the products share their activation matrix, else
     // one w4a16_gemm per problem, in order, on the stream (x rows of K
     // elements)
@@ -242,6 +252,11 @@ extern "C" int w4a16_gemm_grouped(const w4a16_problem* problems, int count, int 
       void* scratch;
       size_t scratch_bytes;
       split_workspace(workspace, workspace_bytes, &counters, &scratch, &scratch_bytes);
+      if (M <= kSmallM) {
+        // 49..64 rows: every weight dequantized once for all rows
+        const int rrc = w4_rows_launch(problems, sxm, nullptr, count, x_dtype, M, counters, scratch, scratch_bytes, st);
+        if (rrc != W4_ERR_UNSUPPORTED) return rrc;
+      }
       const int drc = w4_decode_launch(problems, sxm, nullptr, count, x_dtype, kDecodeM, counters, scratch,
                                        scratch_bytes, st, mr);
       if (drc != W4_ERR_UNSUPPORTED) return drc;

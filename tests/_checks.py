@@ -12,8 +12,9 @@ Tolerances (stated per the task's floating-point bar):
   (tests/test_kernels.py:60): rtol 2e-2, atol 2e-2 * max |ref|.
 
 The decode regime (M <= 64, or M <= 128 with N <= 4096 for a lone product
-or for every product of a grouped call; group size >= 32, dense activation
-rows) applies
+or for every product of a grouped call, except grouped calls of 49..64 rows
+that the several-row kernel takes, see ``_rows``; group size >= 32, dense
+activation rows) applies
 scales and zero points after the matrix-core sums, so it multiplies by the
 exact fp32 W_hat instead of W_hat rounded to the activation dtype.  Its
 elementwise check is against ref = x @ W_hat_fp32^T with
@@ -34,12 +35,50 @@ DEV = "cuda"
 U_OUT = {torch.bfloat16: 2.0**-8, torch.float16: 2.0**-11}
 
 
+def _rows(M: int, G: int, N: int, K: int) -> bool:
+    """True when a product of a grouped call of 49..64 rows on dense aligned
+    rows fits the several-row kernel (w4_rows.hip, rows_plan), which rounds
+    W_hat to the activation dtype: group >= 32, N a multiple of 4, K a
+    multiple of 128 cut into at most 8 parts of at most 2048 (each a multiple
+    of 128)."""
+    if not (49 <= M <= 64 and G >= 32 and N >= 4 and N % 4 == 0 and K % 128 == 0):
+        return False
+    ks = 1
+    while K // ks > 2048:
+        ks *= 2
+    return ks <= 8 and K % (128 * ks) == 0
+
+
 def _decode(M: int, G: int, N: int = 1 << 30, K: int = 1 << 30) -> bool:
     """True when a lone w4a16_matmul takes the factored decode kernel (dense,
-    aligned rows, group >= 32): M <= 16 directly, 17 <= M <= 64 as slices of
-    at most 16 rows in one decode launch, and 65 <= M <= 128 the same way
-    when N <= 4096."""
+    aligned rows, group >= 32; exact fp32 W_hat): M <= 16 directly,
+    17 <= M <= 64 as slices of at most 16 rows in one decode launch, and
+    65 <= M <= 128 the same way when N <= 4096."""
     return G >= 32 and (M <= 64 or (M <= 128 and N <= 4096))
+
+
+def _rows_workgroups(probs) -> int:
+    """Workgroups of the several-row kernel's launch (rows_plan): 128-column
+    tiles x K parts of at most 2048."""
+    total = 0
+    for N, K, G in probs:
+        ks = 1
+        while K // ks > 2048:
+            ks *= 2
+        total += -(-N // 128) * ks
+    return total
+
+
+def _grouped_exact(M: int, probs) -> bool:
+    """The same for w4a16_matmul_grouped over problems (N, K, G), all with
+    group >= 32 and dense rows: 49..64 rows take the several-row kernel when
+    every problem fits it and the launch has at least three quarters of the
+    MI355X's 256 CUs in workgroups, else the decode launch's row slices."""
+    if M <= 48:
+        return True
+    if M <= 64:
+        return not (all(_rows(M, G, N, K) for N, K, G in probs) and _rows_workgroups(probs) >= 192)
+    return M <= 128 and all(N <= 4096 for N, K, G in probs)
 
 
 def _check(out: torch.Tensor, x: torch.Tensor, qw, s, z, ref_unrounded: bool = True, exact_w=False):

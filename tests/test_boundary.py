@@ -5,6 +5,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 import torch
 import torch.nn as nn
@@ -216,3 +217,102 @@ def test_pf3_loads_stay_inside_their_tensors(N, K, G, NW):
     # above would catch a regression of the mask
     (rq, nq), _ = _pf3_max_reach(N, K, G, NW, False, mask_cols=False)
     assert rq > nq
+
+
+def _rows_model(M, N, K, G, ks, MR, sxm=None):
+    """Model of rows_tile's addressing (w4_rows.hip: x_lane, w_lane, sz_lane,
+    a_off, `issue_ring`, the packed-word loads and the partial-tile stores),
+    for every workgroup (column
+    tile, K part), wave, lane and step, including the ring's prefetches past
+    the end of a run (offset | 0x80000000, rejected by the range check).
+    Returns a dict of the largest end reached per tensor / LDS area against its
+    size, the k8 rows each column of a tile reads (each must be read exactly
+    once), and whether every A-fragment read finds the (row, k chunk) the
+    MFMA expects at that LDS position."""
+    OOB, RING, KWAVES, HALVES = 0x80000000, 4, 4, 2
+    WAVES, TILE = KWAVES * HALVES, 64 * HALVES
+    sxm = K if sxm is None else sxm
+    RB, SLOT = MR // 16, MR * 64
+    S = K // (ks * KWAVES * 32)
+    qw_bytes, sz_bytes, x_bytes = K // 8 * N * 4, K // G * N * 2, ((M - 1) * sxm + K) * 2
+    lds_bytes = WAVES * RING * SLOT
+    reach = {"qw": 0, "sz": 0, "x": 0, "lds": 0, "red": 0}
+    k8_reads = np.zeros((K // 8, N), np.int64)
+    lane = np.arange(64)
+    lq, lr = lane & 15, lane >> 4
+    layout_ok = True
+    for ct in range(-(-N // TILE)):
+        for kp in range(ks):
+            for wv in range(WAVES):
+                n0 = ct * TILE + 64 * (wv % HALVES)
+                col_in = n0 + 4 * lq < N
+                col_oob = np.where(col_in, 0, OOB)
+                w_lane = (lr * N + n0 + 4 * lq) * 4
+                sz_lane = (n0 + 4 * lq) * 2
+                st0 = (kp * KWAVES + wv // HALVES) * S
+                ring = wv * RING * SLOT
+                x_lane = []
+                for j in range(RB):
+                    row = 16 * j + (lane >> 2)
+                    c = (lane & 3) ^ ((lane >> 3) & 3)
+                    x_lane.append(np.where(row < M, (row * sxm + c * 8) * 2, OOB))
+                for i in range(S + RING):
+                    oob = 0 if i < S else OOB
+                    st = st0 + min(i, S - 1)
+                    slot = ring + (i & (RING - 1)) * SLOT
+                    for j in range(RB):
+                        vo = (x_lane[j] + st * 64) | oob
+                        ok = vo < x_bytes
+                        if ok.any():
+                            reach["x"] = max(reach["x"], int((vo[ok] + 16).max()))
+                        reach["lds"] = max(reach["lds"], slot + 1024 * j + 16 * 63 + 16)
+                    so = ((st * 32 // G) * N * 2 + sz_lane) | col_oob | oob
+                    ok = so < sz_bytes
+                    if ok.any():
+                        reach["sz"] = max(reach["sz"], int((so[ok] + 8).max()))
+                for i in range(16):  # packed words: every step of the run at once (kRowsMaxWaveSteps)
+                    oob = 0 if i < S else OOB
+                    st = st0 + min(i, S - 1)
+                    wo = (w_lane + st * 16 * N) | col_oob | oob
+                    ok = wo < qw_bytes
+                    if ok.any():
+                        reach["qw"] = max(reach["qw"], int((wo[ok] + 16).max()))
+                        # the words each lane multiplies: k8 row 4 st + lr, columns n0 + 4 lq .. + 3
+                        for l in np.nonzero(ok)[0]:
+                            k8_reads[4 * st + lr[l], n0 + 4 * lq[l]: n0 + 4 * lq[l] + 4] += 1
+                # A fragments: where the stores above put (row, chunk), the reads find it
+                pos = {}
+                for j in range(RB):
+                    for l in range(64):
+                        row = 16 * j + (l >> 2)
+                        pos[1024 * j + 16 * l] = (row, (l & 3) ^ ((l >> 3) & 3))
+                for rb in range(RB):
+                    for l in range(64):
+                        a_off = (l & 15) * 64 + (((l >> 4) ^ (((l & 15) >> 1) & 3)) * 16)
+                        layout_ok = layout_ok and pos[rb * 1024 + a_off] == (16 * rb + (l & 15), l >> 4)
+                # partial tile: row 16 rb + 4 lr + r, columns 4 lq .. + 3 (floats)
+                for rb in range(RB):
+                    for r in range(4):
+                        end = wv * MR * 64 + (16 * rb + 4 * lr + r) * 64 + 4 * lq + 4
+                        reach["red"] = max(reach["red"], int(end.max()) * 4)
+    sizes = {"qw": qw_bytes, "sz": sz_bytes, "x": x_bytes, "lds": lds_bytes, "red": lds_bytes}
+    return reach, sizes, k8_reads, layout_ok
+
+
+@pytest.mark.parametrize("M,N,K,G,ks,MR", [
+    (49, 68, 128, 32, 1, 64), (55, 200, 512, 128, 1, 64), (64, 128, 1024, 64, 2, 64),
+    (50, 2052, 256, 256, 2, 64), (63, 4, 4096, 4096, 8, 64), (64, 1000, 2048, 128, 4, 64),
+    (64, 2048, 8192, 128, 4, 64),
+])
+def test_rows_kernel_accesses_stay_inside_and_cover_k(M, N, K, G, ks, MR):
+    """The several-row kernel: every load's bytes lie inside its tensor (also in
+    a partial last column tile and for the ring's prefetches past a run), LDS
+    stores and reads stay inside the workgroup's array, every (k8 row, column)
+    of the product is read exactly once over the K parts and waves, and the
+    swizzled activation slots give each lane the row and k chunk its MFMA
+    operand needs."""
+    reach, sizes, k8_reads, layout_ok = _rows_model(M, N, K, G, ks, MR)
+    for name in reach:
+        assert reach[name] <= sizes[name], (name, reach[name], sizes[name])
+    assert (k8_reads == 1).all()
+    assert layout_ok

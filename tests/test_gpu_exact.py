@@ -286,6 +286,36 @@ def test_exact_row_slices(M, N, K, G, dt):
     _assert_bits(outs[1], _exact_y(M, 512, 2048, G, 8200, 8300 + M), dt, f"slices grouped partner M={M}")
 
 
+# grouped calls of 49..64 rows: the several-row kernel (every weight
+# dequantized once for all rows) when every problem fits it and the launch
+# fills most of the chip (each case has a wide filler problem for that) -- a
+# partial last 128-column tile, K parts of 2048 finished by the last part to
+# arrive (2, 4, 8 parts), short K, every group class; with one problem it
+# does not take (N not a multiple of 4) the whole call goes to the decode
+# kernel's slices
+ROWS = [  # M, [(N, K, G), ...]
+    (49, [(1000, 4096, 32), (136, 2048, 64), (22528, 2048, 128)]),
+    (57, [(520, 8192, 256), (4, 16384, 1024), (21504, 2048, 32)]),
+    (64, [(2048, 8192, 128), (1032, 1024, 64), (8, 128, 32), (16384, 2048, 128)]),
+    (60, [(2048, 2048, 128), (73, 256, 32), (22528, 2048, 128)]),
+]
+
+
+@pytest.mark.parametrize("dt", ["bf16", "fp16"])
+@pytest.mark.parametrize("M,probs", ROWS)
+def test_exact_rows_grouped(M, probs, dt):
+    print(f"[exact rows] M={M} {probs} {dt}", flush=True)
+    ws, xs, ys = [], [], []
+    for i, (N, K, G) in enumerate(probs):
+        _bound_ok(K)
+        ws.append(_to_dev_weights(N, K, G, seed=9000 + N + K + G))
+        xs.append(_to_dev_x(_exact_x_np(M, K, seed=9100 + M + i), dt))
+        ys.append(_exact_y(M, N, K, G, 9000 + N + K + G, 9100 + M + i))
+    for _ in range(2):  # repeat: arrival counters left at zero, partial tiles rewritten
+        for i, (out, y) in enumerate(zip(int4_hip.w4a16_matmul_grouped(xs, ws), ys)):
+            _assert_bits(out, y, dt, f"rows grouped M={M} problem {i} {probs[i]} {dt}")
+
+
 @pytest.mark.parametrize("dt", ["bf16", "fp16"])
 @pytest.mark.parametrize("M,N,K,G,layout", SIDE)
 def test_exact_side_routes(M, N, K, G, layout, dt):

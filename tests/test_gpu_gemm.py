@@ -8,7 +8,7 @@ import pytest
 import torch
 
 import int4_hip
-from _checks import DEV, _check, _decode, _weights
+from _checks import DEV, _check, _decode, _grouped_exact, _weights
 from _synth import randn
 
 pytestmark = pytest.mark.gpu
@@ -99,12 +99,13 @@ def test_grouped_matches_single(M):
     ws = [_weights(N, K, 128, seed=i) for i, (N, K) in enumerate(shapes)]
     xs = [randn((M, K), seed=50 + i).to(DEV) for i, (N, K) in enumerate(shapes)]
     outs = int4_hip.w4a16_matmul_grouped(xs, ws)
+    ew = _grouped_exact(M, [(N, K, 128) for N, K in shapes])
     for x, (qw, s, z), y in zip(xs, ws, outs):
-        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=ew)
     singles = [int4_hip.w4a16_matmul(x, *w) for x, w in zip(xs, ws)]
-    for x, (qw, s, z), b in zip(xs, ws, singles):
+    for x, (qw, s, z), b, (N, K) in zip(xs, ws, singles, shapes):
         # a lone product may take other tiles (another summation order)
-        _check(b, x, qw, s, z, ref_unrounded=False, exact_w=True)
+        _check(b, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, 128, N, K))
     again = int4_hip.w4a16_matmul_grouped(xs, ws)
     for a, b in zip(outs, again):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
@@ -175,7 +176,7 @@ def test_regimes_share_one_workspace():
     xs = {M: randn((M, 8192), seed=60 + M).to(DEV) for M in (1, 16, 40)}
     first = {M: int4_hip.w4a16_matmul(x, qw, s, z) for M, x in xs.items()}
     for M in (1, 16, 40):
-        _check(first[M], xs[M], qw, s, z, ref_unrounded=False, exact_w=_decode(M, 128))
+        _check(first[M], xs[M], qw, s, z, ref_unrounded=False, exact_w=_decode(M, 128, 2048, 8192))
     for _ in range(3):
         for M in (16, 1, 40, 1):
             assert torch.equal(int4_hip.w4a16_matmul(xs[M], qw, s, z).view(torch.int16), first[M].view(torch.int16))
@@ -192,10 +193,12 @@ def test_decode_ragged_shapes(M, dtype, G):
     ws = [_weights(N, K, G, seed=70 + i) for i, (N, K) in enumerate(shapes)]
     xs = [randn((M, K), seed=80 + i, dtype=dtype).to(DEV) for i, (N, K) in enumerate(shapes)]
     outs = int4_hip.w4a16_matmul_grouped(xs, ws)
-    for x, (qw, s, z), y in zip(xs, ws, outs):
-        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+    ew = _grouped_exact(M, [(N, K, G) for N, K in shapes])
+    for x, (qw, s, z), y, (N, K) in zip(xs, ws, outs, shapes):
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=ew)
         # alone a product may take another tiling (another summation order)
-        _check(int4_hip.w4a16_matmul(x, qw, s, z), x, qw, s, z, ref_unrounded=False, exact_w=True)
+        _check(int4_hip.w4a16_matmul(x, qw, s, z), x, qw, s, z, ref_unrounded=False,
+               exact_w=_decode(M, G, N, K))
 
 
 # one-workgroup-per-CU tilings (M <= 4): 128 columns (K <= 2048, short runs at
@@ -216,10 +219,12 @@ def test_decode_cu_tiles(dtype, G, M):
     ws = [_weights(N, K, G, seed=90 + i) for i, (N, K) in enumerate(shapes)]
     xs = [randn((M, K), seed=100 + i, dtype=dtype).to(DEV) for i, (N, K) in enumerate(shapes)]
     outs = int4_hip.w4a16_matmul_grouped(xs, ws)
-    for x, (qw, s, z), y in zip(xs, ws, outs):
-        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=True)
+    ew = _grouped_exact(M, [(N, K, G) for N, K in shapes])
+    for x, (qw, s, z), y, (N, K) in zip(xs, ws, outs, shapes):
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=ew)
         # alone, a small product takes narrower tiles (another summation order)
-        _check(int4_hip.w4a16_matmul(x, qw, s, z), x, qw, s, z, ref_unrounded=False, exact_w=True)
+        _check(int4_hip.w4a16_matmul(x, qw, s, z), x, qw, s, z, ref_unrounded=False,
+               exact_w=_decode(M, G, N, K))
 
 
 # prefill (M > 64) on dense rows: split-K with fp32 partials for small M x N,
@@ -491,7 +496,7 @@ def test_decode_rows_ksplit(M, N, K, G):
     qw, s, z = _weights(N, K, G, seed=3 * N + K + G)
     x = randn((M, K), seed=M + K).to(DEV)
     first = int4_hip.w4a16_matmul(x, qw, s, z)
-    _check(first, x, qw, s, z, ref_unrounded=False, exact_w=True)
+    _check(first, x, qw, s, z, ref_unrounded=False, exact_w=_decode(M, G, N, K))
     for _ in range(3):
         _poison_workspace()
         again = int4_hip.w4a16_matmul(x, qw, s, z)
@@ -567,7 +572,8 @@ def test_random_grouped_against_oracle(M, K, G, Ns, shared):
     else:
         xs = [randn((M, K), seed=610 + M + i).to(DEV) for i in range(len(Ns))]
     if M <= 64 or (M <= 128 and all(N <= 4096 for N in Ns)):
-        ew = True        # one decode launch (group sizes >= 32)
+        # one several-row or decode launch (group sizes >= 32)
+        ew = _grouped_exact(M, [(N, K, G) for N in Ns])
     elif M > 128:
         ew = False       # prefill kernels (shared or one call per problem)
     else:

@@ -132,7 +132,7 @@ def test_int4linear_from_reference_written_buffers():
         print(f"[golden buffers] M={M}", flush=True)
         x = randn((M, K), seed=40 + M).to(DEV)
         _check(layer(x), x, layer.qweight, layer.scales, layer.zeros, ref_unrounded=False,
-               exact_w=_decode(M, K // s.shape[0]))
+               exact_w=_decode(M, K // s.shape[0], N, K))
 
 
 # ------------------------------------------------- full-size Llama-3.2-1B
