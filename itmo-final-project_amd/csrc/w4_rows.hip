@@ -358,7 +358,14 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
     RowsGroupedArgs g) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kRowsWaves * kRowsRing * MR * 64];
   __shared__ unsigned arrived;
-  const int t = blockIdx.x;
+  // Workgroups go to the 8 XCDs round-robin by index; XCD x takes the x-th
+  // contiguous run of the tile order instead, so each XCD works on one to
+  // three problems and its L2 fetches only their activation blocks (at
+  // M = 64 each is 256 KB to 1 MB and is read by every column tile).
+  const int W = g.wg_start[W4_MAX_GROUPED];
+  const int q8 = W >> 3, r8 = W & 7;
+  const int xcd = (int)blockIdx.x & 7;
+  const int t = xcd * q8 + min(xcd, r8) + ((int)blockIdx.x >> 3);
   int p = 0;
 #pragma unroll
   for (int i = 1; i < W4_MAX_GROUPED; ++i)
