@@ -112,6 +112,7 @@ __device__ __forceinline__ u32x4 rows_lds_read16(uint32_t lds_addr) {
 template <int DT, int MR>
 __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int tile, uint8_t* smem, unsigned* arrived) {
   typedef typename Act<DT>::frag F;
+  static_assert(MR == 64, "the host launches 64-row tiles only");
   constexpr int RB = MR / 16;                  // row blocks of 16
   constexpr int SLOT = MR * 64;                // bytes of a step's activations: MR rows x 32 k
   constexpr int WAVE_LDS = kRowsRing * SLOT;   // one wave's ring = its MR x 64 fp32 partial tile
@@ -234,13 +235,10 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int tile, uin
       u32x4 ar[RB];
       ar[0] = rows_lds_read16<SO>(a_lds);
       ar[1] = rows_lds_read16<SO + 1024>(a_lds);
-      if constexpr (RB == 4) {
-        ar[2] = rows_lds_read16<SO + 2048>(a_lds);
-        ar[3] = rows_lds_read16<SO + 3072>(a_lds);
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ar[0]), "+v"(ar[1]), "+v"(ar[2]), "+v"(ar[3]));
-      } else {
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ar[0]), "+v"(ar[1]));
-      }
+      ar[2] = rows_lds_read16<SO + 2048>(a_lds);
+      ar[3] = rows_lds_read16<SO + 3072>(a_lds);
+      // the reads' results are tied to the wait, so no use moves above it
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(ar[0]), "+v"(ar[1]), "+v"(ar[2]), "+v"(ar[3]));
       const SZ& r = szr[SL];
       if (i == 0 || (((uint32_t)(st0 + i) * 32u) & gmask) == 0) {  // first step of a group (uniform)
 #pragma unroll
