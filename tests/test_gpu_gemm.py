@@ -436,6 +436,32 @@ def test_capture_grouped_without_warmup():
             torch.randn(1 << 16, device=DEV).sum().item()
 
 
+def test_capture_grouped_block_m64_rows():
+    """The 7-linear block at M = 64 in one grouped call takes the several-row
+    kernel, whose down_proj K split needs the workspace: checked against the
+    oracle (W_hat rounded to bf16), then captured without a warm-up and
+    replayed with eager work between replays, every replay equal to the eager
+    bits."""
+    shapes = [(2048, 2048), (512, 2048), (512, 2048), (2048, 2048), (8192, 2048), (8192, 2048), (2048, 8192)]
+    assert not _grouped_exact(64, [(N, K, 128) for N, K in shapes])  # the several-row kernel's route
+    ws = [_weights(N, K, 128, seed=600 + i) for i, (N, K) in enumerate(shapes)]
+    xs = [randn((64, K), seed=610 + i).to(DEV) for i, (N, K) in enumerate(shapes)]
+    eager = int4_hip.w4a16_matmul_grouped(xs, ws)
+    for x, (qw, s, z), y in zip(xs, ws, eager):
+        _check(y, x, qw, s, z, ref_unrounded=False, exact_w=False)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = int4_hip.w4a16_matmul_grouped(xs, ws)
+    for _ in range(3):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, eager):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+        torch.randn(1 << 16, device=DEV).sum().item()
+
+
 # strided activation rows (row stride not a multiple of 8) take the skinny
 # split-K kernel even at M <= 16; a fresh stream sizes its workspace from the
 # size query, which must cover that route too
