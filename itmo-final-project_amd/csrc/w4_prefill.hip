@@ -749,7 +749,8 @@ __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2)
 //    of one k8 row per thread), dequantize them exactly as pf3 does (fp32
 //    (q - z) * s, one rounding to the activation dtype) and store the bf16 /
 //    fp16 B tile to LDS, column-major with 16-byte chunk (column n, k8 row j)
-//    at slot n * 8 + (j ^ ((n >> 1) & 7)); the activation tile arrives by
+//    at slot n * 8 + (j ^ ((n >> 1) & 7)) (TS = 128: j ^ (((n >> 2) ^ (n << 1))
+//    & 7), below); the activation tile arrives by
 //    direct-to-LDS loads in pf3's swizzled layout, so the A and B fragment
 //    reads (32 rows / columns x one chunk per 16 lanes) hit all banks.
 //  * KP sets (KP = 1, 2 or 4 per workgroup, 4 to 16 waves) run the same tile
@@ -836,10 +837,19 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   const int wc = WPT * (tid & 31);  // first of its WPT adjacent columns
   const uint32_t w_off = ((uint32_t)wj * (uint32_t)N + (uint32_t)(n0 + wc)) * 4u;
   const uint32_t sz_off = (uint32_t)(n0 + wc) * 2u;
-  // weight chunk (column n, k8 row wj) of a buffer, elements
+  // weight chunk (column n, k8 row j) of a buffer at slot n * 8 + (j ^ bswz(n)),
+  // elements.  A 128-bit LDS write serves 8 lanes at a time, a 128-bit read 16
+  // lanes over the 64 banks (even and odd columns in the two bank halves).
+  // TS = 64: the 8 lanes of a store hold columns 2l + i, and (n >> 1) & 7
+  // gives them 8 distinct chunks, as it gives the 8 even (odd) columns of a
+  // fragment read.  TS = 128: a store's 8 lanes hold columns 4l + i, where
+  // (n >> 1) & 7 takes only 4 values (a two-way conflict on every store);
+  // ((n >> 2) ^ (n << 1)) & 7 is distinct over both sets.  Both depend on
+  // n % 32 only, so blocks 32 columns apart share the offsets.
+  auto bswz = [](int n) { return TS == 64 ? ((n >> 1) & 7) : (((n >> 2) ^ (n << 1)) & 7); };
   int b_off[WPT];
 #pragma unroll
-  for (int i = 0; i < WPT; ++i) b_off[i] = ((wc + i) * 8 + (wj ^ (((wc + i) >> 1) & 7))) * 8;
+  for (int i = 0; i < WPT; ++i) b_off[i] = ((wc + i) * 8 + (wj ^ bswz(wc + i))) * 8;
   const uint32_t magic = fp16_magic_vgpr();
 
   struct Regs {
@@ -893,9 +903,12 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
     for (int j = 0; j < WB; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-  int f_off[4];
+  int f_off[4], fb_off[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) f_off[ks] = (l32 * 8 + ((2 * ks + lh) ^ ((l32 >> 1) & 7))) * 8;
+  for (int ks = 0; ks < 4; ++ks) {
+    f_off[ks] = (l32 * 8 + ((2 * ks + lh) ^ ((l32 >> 1) & 7))) * 8;
+    fb_off[ks] = TS == 64 ? f_off[ks] : (l32 * 8 + ((2 * ks + lh) ^ bswz(l32))) * 8;
+  }
   // blocks 32 rows / columns apart have the same swizzle: an immediate offset
   auto multiply = [&](int slot) {
     const uint16_t* A = As + slot * ASLOT + wm * (TS / 2) * PF2_BK;
@@ -906,7 +919,7 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
 #pragma unroll
       for (int i = 0; i < WB; ++i) {
         af[i] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(A + i * 32 * PF2_BK + f_off[ks]));
-        bf[i] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(B + i * 32 * PF2_BK + f_off[ks]));
+        bf[i] = __builtin_bit_cast(F, *reinterpret_cast<const u32x4*>(B + i * 32 * PF2_BK + fb_off[ks]));
       }
 #pragma unroll
       for (int i = 0; i < WB; ++i)
