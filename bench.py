@@ -776,9 +776,10 @@ def main() -> int:
         kern_ms = ms_per_step
         achieved = bytes1 / (kern_ms * 1e-3) / 1e9
         # steady state beside it: a graph of the 16 sets replayed back to back
+        # (median of five runs of 10 replays, so one disturbed run does not set it)
         g_main = graph_of(lambda: [grouped(i)() for i in range(nsets)], stream)
         time_graph(g_main, 2, stream)
-        steady_ms = time_graph(g_main, 10, stream) / nsets
+        steady_ms = sorted(time_graph(g_main, 10, stream) for _ in range(5))[2] / nsets
         del g_main
 
     # ------------------------------------------------- M=1 per-linear launches (reference-comparable)
