@@ -83,6 +83,7 @@ constexpr int kRowsMinM = 49;  // fewer rows: the decode kernel's 16-row slices
 constexpr uint32_t kRowsOOB = 0x80000000u;  // offset the buffer range check rejects
 constexpr int kRowsBufFlags = 0x00020000;   // raw buffer, 32-bit data format
 constexpr int kRowsStreamAux = 2;           // nt: the packed words are read once per call
+constexpr int kRowsCoherentAux = 16;        // sc1: the cache policy of agent-scope atomic loads and stores
 
 __device__ __forceinline__ void rows_lds_load16(__amdgpu_buffer_rsrc_t r, uint8_t* lds, uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voffset, 0, 0, 0);
@@ -293,19 +294,22 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int tile, uin
     // have completed, count the arrival; the last part sums every part in
     // part order (so the result does not depend on which part is last),
     // writes y and leaves the counter at zero
+    // The partial tiles move as 128-bit buffer accesses with the sc1 policy,
+    // the policy the compiler gives agent-scope atomic loads and stores
+    // (written through to, and read from, the point all XCDs share); their
+    // order against the arrival counter comes from the waits and barriers
+    // below, as for atomics.
     constexpr int E = MR * kRowsTile;
     float* const tiles = a.part + (int64_t)ct * ks * E;
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc((void*)tiles, (short)0, ks * E * (int)sizeof(float), kRowsBufFlags);
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
       const int q = tid + u * kRowsWaves * 64;
-      unsigned long long* d = reinterpret_cast<unsigned long long*>(tiles + kp * E + 4 * q);
       // (the whole vector is bit-cast: a bit cast of one element of an
       // ext_vector_type value reads the vector's first element)
-      const u32x4 b = __builtin_bit_cast(u32x4, v[u]);
-      const unsigned long long lo = (unsigned long long)b[0] | ((unsigned long long)b[1] << 32);
-      const unsigned long long hi = (unsigned long long)b[2] | ((unsigned long long)b[3] << 32);
-      __hip_atomic_store(d, lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(d + 1, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[u]), rp, (uint32_t)(kp * E + 4 * q) * 4u, 0,
+                                             kRowsCoherentAux);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -313,26 +317,23 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int tile, uin
     __syncthreads();
     if (*arrived != (unsigned)(ks - 1)) return;
     if (tid == 0) __hip_atomic_store(a.cnt + ct, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every part's tile is requested before the first add
+    u32x4 other[QPT][kMaxRowsSplit];
 #pragma unroll
     for (int u = 0; u < QPT; ++u) {
       const int q = tid + u * kRowsWaves * 64;
-      unsigned long long lo[kMaxRowsSplit], hi[kMaxRowsSplit];
 #pragma unroll
-      for (int p = 0; p < kMaxRowsSplit; ++p) {
-        const unsigned long long* d = reinterpret_cast<const unsigned long long*>(tiles + p * E + 4 * q);
-        const bool other = p < ks && p != kp;
-        lo[p] = other ? __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-        hi[p] = other ? __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0ull;
-      }
+      for (int p = 0; p < kMaxRowsSplit; ++p)
+        if (p < ks && p != kp)
+          other[u][p] = __builtin_amdgcn_raw_buffer_load_b128(rp, (uint32_t)(p * E + 4 * q) * 4u, 0, kRowsCoherentAux);
+    }
+#pragma unroll
+    for (int u = 0; u < QPT; ++u) {
       f32x4 sum = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int p = 0; p < kMaxRowsSplit; ++p) {
         if (p < ks) {
-          const f32x4 t = p == kp ? v[u]
-                                  : f32x4{__builtin_bit_cast(float, (uint32_t)lo[p]),
-                                          __builtin_bit_cast(float, (uint32_t)(lo[p] >> 32)),
-                                          __builtin_bit_cast(float, (uint32_t)hi[p]),
-                                          __builtin_bit_cast(float, (uint32_t)(hi[p] >> 32))};
+          const f32x4 t = p == kp ? v[u] : __builtin_bit_cast(f32x4, other[u][p]);
           sum = p == 0 ? t : sum + t;
         }
       }
