@@ -134,6 +134,7 @@ constexpr int kDecBufFlags = 0x00020000;   // raw buffer, 32-bit data format
 // are read once per call as well and take the same policy (M = 1 block
 // 9.5 -> 9.2 us with both).
 constexpr int kDecWeightAux = 2;
+constexpr int kDecCoherentAux = 16;  // sc1: the cache policy of agent-scope atomic loads and stores
 
 template <int DT>
 struct DecNum;
@@ -821,13 +822,16 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
       if (ks > 1) {
         // K split: publish the pair (one 64-bit device-coherent store), count
         // the part's arrival; the last part sums every part in part order
+        // (the pair moves as a 64-bit buffer access with the sc1 policy, the
+        // policy of agent-scope atomic loads and stores, ordered against the
+        // arrival counter by the waits and barriers below)
         constexpr int E = MR * TW;
         unsigned* const cnt = a.cnt + (int64_t)sl * (a.col_tiles >> ks_log);
         float* const tiles = a.part + (int64_t)sl * a.col_tiles * E + (int64_t)ct * ks * E;
-        const unsigned long long mine =
-            (unsigned long long)__builtin_bit_cast(uint32_t, vx) | ((unsigned long long)__builtin_bit_cast(uint32_t, vy) << 32);
-        __hip_atomic_store(reinterpret_cast<unsigned long long*>(tiles + kp * E + el), mine, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+        const __amdgpu_buffer_rsrc_t rp =
+            __builtin_amdgcn_make_buffer_rsrc((void*)tiles, (short)0, ks * E * (int)sizeof(float), kDecBufFlags);
+        const u32x2 mine = u32x2{__builtin_bit_cast(uint32_t, vx), __builtin_bit_cast(uint32_t, vy)};
+        __builtin_amdgcn_raw_buffer_store_b64(mine, rp, (uint32_t)(kp * E + el) * 4u, 0, kDecCoherentAux);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();  // every partial of this part has completed; red is no longer read
         unsigned* const arrived = reinterpret_cast<unsigned*>(lds);
@@ -835,19 +839,21 @@ __device__ __forceinline__ void dec_tile_one(const DecArgs& a, int tile, uint8_t
         __syncthreads();
         if (*arrived != (unsigned)(ks - 1)) return;
         if (tid == 0) __hip_atomic_store(cnt + ct, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        unsigned long long other[kMaxKSplit];
+        u32x2 other[kMaxKSplit];
 #pragma unroll
         for (int q = 0; q < kMaxKSplit; ++q)
           other[q] = (q < ks && q != kp)
-                         ? __hip_atomic_load(reinterpret_cast<unsigned long long*>(tiles + q * E + el), __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT)
+                         ? __builtin_amdgcn_raw_buffer_load_b64(rp, (uint32_t)(q * E + el) * 4u, 0, kDecCoherentAux)
                          : mine;
         vx = 0.0f, vy = 0.0f;
 #pragma unroll
         for (int q = 0; q < kMaxKSplit; ++q)
           if (q < ks) {
-            vx += __builtin_bit_cast(float, (uint32_t)other[q]);
-            vy += __builtin_bit_cast(float, (uint32_t)(other[q] >> 32));
+            // (the whole vector is bit-cast: a bit cast of one element of an
+            // ext_vector_type value reads the vector's first element)
+            const float2 f = __builtin_bit_cast(float2, other[q]);
+            vx += f.x;
+            vy += f.y;
           }
       }
       if (m < M && n < N) {
