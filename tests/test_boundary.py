@@ -316,3 +316,46 @@ def test_rows_kernel_accesses_stay_inside_and_cover_k(M, N, K, G, ks, MR):
         assert reach[name] <= sizes[name], (name, reach[name], sizes[name])
     assert (k8_reads == 1).all()
     assert layout_ok
+
+
+def _pf5_swizzle(TS: int, n: int) -> int:
+    """The chunk swizzle of pf5's dequantized weight tile (w4_prefill.hip,
+    pf5_kernel): chunk (column n, k8 row j) of a buffer at slot n * 8 + (j ^ f(n))."""
+    return (n >> 1) & 7 if TS == 64 else ((n >> 2) ^ (n << 1)) & 7
+
+
+@pytest.mark.parametrize("TS", [64, 128])
+def test_pf5_weight_tile_swizzle_is_conflict_free(TS):
+    """pf5's LDS weight tile under the bank model its layout is chosen for (64
+    banks of 4 bytes; a 128-bit store serves 8 lanes at a time, a 128-bit read
+    16): the slots of a column are a permutation of its 8 chunks; the 8 lanes of
+    a store (thread t writes columns WPT (t % 32) + i of k8 row t / 32) and the
+    16 lanes of a fragment read (consecutive columns, one chunk) cover distinct
+    bank quads; the swizzle depends on n % 32 only (blocks 32 columns apart
+    share the offsets).  The 64-wide form on 128-wide stores is the case that
+    conflicts."""
+    WPT = TS // 32
+
+    def quad(n, j):  # bank quad (4 banks) of chunk (n, j)
+        slot = n * 8 + (j ^ _pf5_swizzle(TS, n))
+        return (slot * 16 // 4 % 64) // 4
+
+    for n in range(TS):
+        assert sorted(j ^ _pf5_swizzle(TS, n) for j in range(8)) == list(range(8))
+        assert _pf5_swizzle(TS, n) == _pf5_swizzle(TS, n % 32)
+    for j in range(8):  # stores: lanes l .. l + 7 of one k8 row
+        for i in range(WPT):
+            for l0 in range(0, 32, 8):
+                quads = [quad(WPT * l + i, j) for l in range(l0, l0 + 8)]
+                assert len(set(quads)) == 8, (TS, j, i, l0, quads)
+    for c in range(8):  # fragment reads: 16 consecutive columns, chunk c
+        for n0 in range(0, TS, 16):
+            banks = set()
+            for n in range(n0, n0 + 16):
+                slot = n * 8 + (c ^ _pf5_swizzle(TS, n))
+                b = slot * 16 // 4 % 64
+                banks.update(range(b, b + 4))
+            assert len(banks) == 64, (TS, c, n0)
+    if TS == 128:  # the 64-wide swizzle on this tile's stores: two-way conflicts
+        old = lambda n, j: ((n * 8 + (j ^ ((n >> 1) & 7))) * 16 // 4 % 64) // 4
+        assert len({old(4 * l, 0) for l in range(8)}) == 4
