@@ -290,15 +290,14 @@ __device__ __forceinline__ void rows_tile(const RowsArgs& a, const int tile, uin
     for (int r = 1; r < kRowsKWaves; ++r) v[u] += pv[r];
   }
   if (ks > 1) {
-    // publish this part's tile with device-coherent stores, wait until they
-    // have completed, count the arrival; the last part sums every part in
-    // part order (so the result does not depend on which part is last),
-    // writes y and leaves the counter at zero
-    // The partial tiles move as 128-bit buffer accesses with the sc1 policy,
-    // the policy the compiler gives agent-scope atomic loads and stores
-    // (written through to, and read from, the point all XCDs share); their
-    // order against the arrival counter comes from the waits and barriers
-    // below, as for atomics.
+    // Publish this part's tile, wait until the stores have completed, count
+    // the arrival; the last part sums every part in part order (so the result
+    // does not depend on which part is last), writes y and leaves the counter
+    // at zero.  The tiles move as 128-bit buffer accesses with the sc1 policy,
+    // the one the compiler gives agent-scope atomic loads and stores (written
+    // through to, and read from, the level all XCDs share); their order
+    // against the arrival counter comes from the waits and barriers, as for
+    // atomics.
     constexpr int E = MR * kRowsTile;
     float* const tiles = a.part + (int64_t)ct * ks * E;
     const __amdgpu_buffer_rsrc_t rp =
