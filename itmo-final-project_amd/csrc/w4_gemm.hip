@@ -22,11 +22,14 @@ int w4_gemv_grouped_launch(const w4a16_problem* problems, int count, int x_dtype
 int64_t w4_gemv_grouped_scratch_bytes(const w4a16_problem* problems, int count, int64_t M);
 int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
-                      void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
+                      void* y, int64_t ldy, void* ws, size_t ws_bytes, unsigned* counters, hipStream_t st);
 size_t w4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K);
 int w4_prefill_fast_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                            int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
-                           void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
+                           void* y, int64_t ldy, void* ws, size_t ws_bytes, unsigned* counters, hipStream_t st);
+bool w4_prefill_split_route(const void* x, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
+                            const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, const void* y,
+                            int64_t ldy);
 
 int w4_rows_launch(const w4a16_problem* problems, const int64_t* sxm, const int64_t* ldy, int count, int x_dtype,
                    int64_t M, unsigned* counters, void* scratch, size_t scratch_bytes, hipStream_t st);
@@ -160,10 +163,12 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
   if (M <= kDecodeM)
     return w4_gemv_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
                           counters, scratch, scratch_bytes, st);
-  if (sliced_lone(M, N) && stride_xk == 1) {
+  if (sliced_lone(M, N) && stride_xk == 1 &&
+      !w4_prefill_split_route(x, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy)) {
     // 17 <= M <= 64 (and up to 128 for N <= 4096): the rows as slices of
     // kDecodeM in one decode launch (the weights are read once per slice, the
-    // repeats mostly from L2): no reduce launch
+    // repeats mostly from L2): no reduce launch.  Rows above 64 with K > 4096
+    // that the prefill kernel's K-split launch takes go there instead.
     const w4a16_problem q{x, qweight, scales, zeros, y, N, K, (int32_t)G, 0};
     const int rc = w4_decode_launch(&q, &stride_xm, &ldy, 1, x_dtype, kDecodeM, counters, scratch, scratch_bytes,
                                     st, &M);
@@ -171,13 +176,13 @@ extern "C" int w4a16_gemm(const void* x, int x_dtype, int64_t M, int64_t N, int6
   }
   if (M <= kSmallM) {
     const int rc = w4_prefill_fast_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros,
-                                          (int)G, y, ldy, scratch, scratch_bytes, st);
+                                          (int)G, y, ldy, scratch, scratch_bytes, counters, st);
     if (rc != W4_ERR_UNSUPPORTED) return rc;
     return w4_skinny_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y,
                             ldy, scratch, scratch_bytes, st);
   }
   return w4_prefill_launch(x, x_dtype, M, N, K, stride_xm, stride_xk, qweight, scales, zeros, (int)G, y, ldy,
-                           scratch, scratch_bytes, st);
+                           scratch, scratch_bytes, counters, st);
 }
 
 static int check_grouped(const w4a16_problem* problems, int count, int64_t M) {

@@ -228,7 +228,13 @@ struct Pf2Args {
   int M, N, K, gshift;
   int tiles_n, tiles_mn, kt_per_split;
   int y16;  // pf3: y rows 16-byte aligned and N % 8 == 0 (LDS-staged 16-byte output stores)
+  // pf5 with 64 x 64 tiles: K cut into ks ranges over as many workgroups
+  // (workgroup t: range t / tiles_mn of tile t % tiles_mn), finished by the
+  // last to arrive (per-tile arrival counters in cnt, partial tiles in ws)
+  int ks;
+  unsigned* cnt;
 };
+constexpr int kMaxPf5Split = 4;
 
 constexpr int PF2_BM = 128;
 constexpr int PF2_BK = 64;
@@ -811,12 +817,15 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   uint16_t* const Bs = As + 2 * ASLOT;
   const int wm = wave >> 1, wn = wave & 1;  // this wave's quarter of the tile
   const int l32 = lane & 31, lh = lane >> 5;
-  const int tile_m = (int)blockIdx.x / a.tiles_n;
-  const int tile_n = (int)blockIdx.x - tile_m * a.tiles_n;
+  const int KS = TS == 64 ? a.ks : 1;  // K ranges across workgroups
+  const int split = KS > 1 ? (int)blockIdx.x / a.tiles_mn : 0;
+  const int tb = (int)blockIdx.x - split * a.tiles_mn;  // the tile
+  const int tile_m = tb / a.tiles_n;
+  const int tile_n = tb - tile_m * a.tiles_n;
   const int m0 = tile_m * TS, n0 = tile_n * TS;
   const int N = a.N;
-  const int KT = a.K / PF2_BK / KP;  // steps of one part (even, >= 2)
-  const int kt0 = kp * KT;
+  const int KT = a.kt_per_split;  // steps of one part (even, >= 2; the host divides K)
+  const int kt0 = (split * KP + kp) * KT;
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)a.x, (short)0, (int)a.x_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)a.qw, (short)0, (int)a.qw_bytes, 0x00020000);
@@ -1008,6 +1017,78 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
     }
     __syncthreads();
   }
+  if constexpr (TS == 64) {
+    if (KS > 1) {
+      // K split across workgroups: part 0's waves publish the workgroup's
+      // sum (their accumulators, lane-major 16-byte chunks) with 128-bit
+      // sc1 stores (the cache policy of agent-scope atomic stores: written
+      // through to the level all XCDs share), wait until they have
+      // completed, and count the arrival; the last range to arrive reads the
+      // others with sc1 loads, sums all ranges in range order (so the
+      // result does not depend on which is last), leaves the counter at zero
+      // and writes the tile.
+      constexpr int C = PER / 4;  // 16-byte accumulator chunks per lane
+      float* const parts = a.ws + (int64_t)tb * KS * (TS * TS);
+      const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void*)parts, (short)0,
+                                                                           KS * TS * TS * (int)sizeof(float), 0x00020000);
+      const uint32_t lane_off = ((uint32_t)(wave * C) * 64u + (uint32_t)lane) * 16u;  // + 1024 c
+      constexpr uint32_t RANGE = TS * TS * sizeof(float);
+      if (kp == 0) {
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const f32x4 v = f32x4{acc[0][0][4 * c], acc[0][0][4 * c + 1], acc[0][0][4 * c + 2], acc[0][0][4 * c + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
+                                                 (uint32_t)split * RANGE + lane_off + 1024u * c, 0, 16);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      // the arrival count goes through the array's last word, which neither
+      // the part sums (its first half) nor, from here on, the rings use (a
+      // second LDS object made the compiler wait for every direct-to-LDS load
+      // in flight before each fragment read of the main loop)
+      unsigned* const arrived = reinterpret_cast<unsigned*>(lds + KP * SET) - 1;
+      if (threadIdx.x == 0)
+        *arrived = __hip_atomic_fetch_add(a.cnt + tb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __syncthreads();
+      if (*arrived != (unsigned)(KS - 1)) return;
+      if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (kp == 0) {
+        // every other range's chunks are requested before the first add:
+        // slot o holds range o + (o >= split), so the registers are indexed
+        // at compile time
+        u32x4 other[kMaxPf5Split - 1][C];
+#pragma unroll
+        for (int o = 0; o < kMaxPf5Split - 1; ++o)
+          if (o < KS - 1) {
+            const uint32_t q = (uint32_t)(o + (o >= split ? 1 : 0));
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+              other[o][c] = __builtin_amdgcn_raw_buffer_load_b128(rp, q * RANGE + lane_off + 1024u * c, 0, 16);
+          }
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+          const f32x4 own = f32x4{acc[0][0][4 * c], acc[0][0][4 * c + 1], acc[0][0][4 * c + 2], acc[0][0][4 * c + 3]};
+          f32x4 sum = own;
+#pragma unroll
+          for (int q = 0; q < kMaxPf5Split; ++q) {
+            if (q < KS) {
+              // range q in range order: slot q below this workgroup's range,
+              // slot q - 1 above it (the whole vector is bit-cast: a bit cast
+              // of one element of an ext_vector_type value reads the vector's
+              // first element)
+              const f32x4 below = __builtin_bit_cast(f32x4, other[q < kMaxPf5Split - 1 ? q : 0][c]);
+              const f32x4 above = __builtin_bit_cast(f32x4, other[q > 0 ? q - 1 : 0][c]);
+              const f32x4 t = q < split ? below : q == split ? own : above;
+              sum = q == 0 ? t : sum + t;
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[0][0][4 * c + e] = sum[e];
+        }
+      }
+    }
+  }
   // output: the tile in LDS (part 0's area), then 16-byte row chunks
   static_assert(TS * TS <= SET, "output tile fits part 0's area");
   uint16_t* T = lds;
@@ -1174,13 +1255,28 @@ void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t 
 //    with four).
 //  * TS = 128 with two parts where it has 0.75 to 1 tile of 128 x 128 per CU
 //    (N % 128 == 0, K % 256 == 0).
+//  * K > 4096 with 64 < M <= 128 (down_proj at M = 128): 64 x 64 tiles of
+//    four parts, K cut into ks ranges of at most 2048 over as many
+//    workgroups while the launch fits one workgroup per CU, finished by the
+//    last range to arrive: down_proj at M = 128 about 14 us against 17 us as
+//    16-row slices (the decode regime's route for these rows otherwise).
 struct Pf5Plan {
-  int parts = 0, ts = 64;
+  int parts = 0, ts = 64, ks = 1;
 };
 Pf5Plan pf5_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
   Pf5Plan p;
-  if (G < 64 || K > 4096 || K % 128 != 0) return p;
   const int64_t cus = device_cu_count();
+  if (K > 4096) {
+    if (G < 64 || M <= 64 || M > 128 || N % 64 != 0) return p;
+    int ks = 2;
+    while (K / ks > 2048) ks *= 2;
+    if (ks <= w4::kMaxPf5Split && K % ks == 0 && (K / ks) % 512 == 0 && (M + 63) / 64 * (N / 64) * ks <= cus) {
+      p.parts = 4;
+      p.ks = ks;
+    }
+    return p;
+  }
+  if (G < 64 || K % 128 != 0) return p;
   if (N % 64 == 0 && (M + 63) / 64 * (N / 64) <= cus) {
     p.parts = (K % 512 == 0 && M <= N) ? 4 : K % 256 == 0 ? 2 : 1;
     return p;
@@ -1193,9 +1289,16 @@ Pf5Plan pf5_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
   return p;
 }
 
+// Partial-tile bytes of a K-split pf5 launch (0 when the shape takes none);
+// the plan does not depend on the group size once it is >= 64.
+size_t pf5_split_scratch(int64_t M, int64_t N, int64_t K) {
+  const Pf5Plan p = pf5_plan(M, N, K, 64);
+  return p.ks > 1 ? (size_t)p.ks * ((M + 63) / 64) * (N / 64) * 64 * 64 * sizeof(float) : 0;
+}
+
 template <int DT>
 void pf5_launch(const Pf5Plan& p, const w4::Pf2Args& a, hipStream_t st) {
-  const dim3 grid((unsigned)(((a.M + p.ts - 1) / p.ts) * (a.N / p.ts)));
+  const dim3 grid((unsigned)(((a.M + p.ts - 1) / p.ts) * (a.N / p.ts) * p.ks));
   if (p.ts == 128)
     hipLaunchKernelGGL((w4::pf5_kernel<DT, 2, 128>), grid, dim3(512), 0, st, a);
   else if (p.parts == 4)
@@ -1212,11 +1315,22 @@ int w4_splitk_reduce_launch(const float* ws, int S, int64_t M, int64_t N, int x_
                             hipStream_t st);
 
 // Scratch bytes (past the workspace's counter area) of a prefill launch.
-size_t w4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K) { return plan_pf2(M, N, K).ws; }
+size_t w4_prefill_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return std::max(plan_pf2(M, N, K).ws, pf5_split_scratch(M, N, K));
+}
+
+// True when w4_prefill_launch takes the K-split pf5 launch for this product
+// (the GEMM entry point then routes such rows here instead of to the decode
+// kernel's row slices).
+bool w4_prefill_split_route(const void* x, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t sxk,
+                            const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G, const void* y,
+                            int64_t ldy) {
+  return pf2_ok(x, M, N, K, sxm, sxk, qw, sc, ze, y, ldy) && pf5_plan(M, N, K, G).ks > 1;
+}
 
 int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
-                      void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st);
+                      void* y, int64_t ldy, void* ws, size_t ws_bytes, unsigned* counters, hipStream_t st);
 
 // The pipelined MFMA kernel for 17 <= M <= 64 as well: returns
 // W4_ERR_UNSUPPORTED (nothing launched, no message) when the activations are
@@ -1224,17 +1338,29 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
 // takes the split-K skinny kernel.
 int w4_prefill_fast_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                            int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
-                           void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st) {
+                           void* y, int64_t ldy, void* ws, size_t ws_bytes, unsigned* counters, hipStream_t st) {
   if (K % w4::PF2_BK != 0 || !pf2_ok(x, M, N, K, sxm, sxk, qw, sc, ze, y, ldy)) return W4_ERR_UNSUPPORTED;
-  return w4_prefill_launch(x, x_dtype, M, N, K, sxm, sxk, qw, sc, ze, G, y, ldy, ws, ws_bytes, st);
+  return w4_prefill_launch(x, x_dtype, M, N, K, sxm, sxk, qw, sc, ze, G, y, ldy, ws, ws_bytes, counters, st);
 }
 
 int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t K, int64_t sxm,
                       int64_t sxk, const int32_t* qw, const uint16_t* sc, const uint16_t* ze, int G,
-                      void* y, int64_t ldy, void* ws, size_t ws_bytes, hipStream_t st) {
+                      void* y, int64_t ldy, void* ws, size_t ws_bytes, unsigned* counters, hipStream_t st) {
   if (pf2_ok(x, M, N, K, sxm, sxk, qw, sc, ze, y, ldy)) {
     if (const Pf5Plan p5 = pf5_plan(M, N, K, G); p5.parts) {
+      const int64_t tiles = ((M + p5.ts - 1) / p5.ts) * (N / p5.ts);
+      if (p5.ks > 1) {
+        const size_t need = (size_t)p5.ks * tiles * p5.ts * p5.ts * sizeof(float);
+        if (counters == nullptr || ws == nullptr || ws_bytes < need)
+          return fail(W4_ERR_WORKSPACE, "w4a16_gemm: workspace of %zu bytes required, %zu given",
+                      (size_t)W4_WORKSPACE_COUNTER_BYTES + need, ws ? ws_bytes : (size_t)0);
+      }
       w4::Pf2Args a{};
+      a.ks = p5.ks;
+      a.tiles_mn = (int)tiles;
+      a.kt_per_split = (int)(K / w4::PF2_BK / p5.parts / p5.ks);
+      a.ws = p5.ks > 1 ? static_cast<float*>(ws) : nullptr;
+      a.cnt = p5.ks > 1 ? counters : nullptr;
       a.x = static_cast<const uint16_t*>(x);
       a.qw = reinterpret_cast<const uint32_t*>(qw);
       a.sc = sc;

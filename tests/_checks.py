@@ -13,8 +13,9 @@ Tolerances (stated per the task's floating-point bar):
 
 The decode regime (M <= 64, or M <= 128 with N <= 4096 for a lone product
 or for every product of a grouped call, except grouped calls of 49..64 rows
-that the several-row kernel takes, see ``_rows``; group size >= 32, dense
-activation rows) applies
+that the several-row kernel takes, see ``_rows``, and lone products of more
+than 64 rows with K > 4096 that the prefill kernel splits, see
+``_pf5_split``; group size >= 32, dense activation rows) applies
 scales and zero points after the matrix-core sums, so it multiplies by the
 exact fp32 W_hat instead of W_hat rounded to the activation dtype.  Its
 elementwise check is against ref = x @ W_hat_fp32^T with
@@ -49,12 +50,27 @@ def _rows(M: int, G: int, N: int, K: int) -> bool:
     return ks <= 8 and K % (128 * ks) == 0
 
 
+def _pf5_split(M: int, G: int, N: int, K: int) -> bool:
+    """True when a lone product of 65..128 dense aligned rows with K > 4096
+    takes the prefill kernel's K-split launch (w4_prefill.hip, pf5_plan;
+    W_hat rounded to the activation dtype): group >= 64, N a multiple of 64,
+    K cut into ks <= 4 ranges of at most 2048 (each a multiple of 512), one
+    workgroup per 64 x 64 tile and range within the MI355X's 256 CUs."""
+    if not (64 < M <= 128 and G >= 64 and N % 64 == 0 and K > 4096):
+        return False
+    ks = 2
+    while K // ks > 2048:
+        ks *= 2
+    return ks <= 4 and K % ks == 0 and (K // ks) % 512 == 0 and -(-M // 64) * (N // 64) * ks <= 256
+
+
 def _decode(M: int, G: int, N: int = 1 << 30, K: int = 1 << 30) -> bool:
     """True when a lone w4a16_matmul takes the factored decode kernel (dense,
     aligned rows, group >= 32; exact fp32 W_hat): M <= 16 directly,
     17 <= M <= 64 as slices of at most 16 rows in one decode launch, and
-    65 <= M <= 128 the same way when N <= 4096."""
-    return G >= 32 and (M <= 64 or (M <= 128 and N <= 4096))
+    65 <= M <= 128 the same way when N <= 4096, unless the product takes the
+    prefill kernel's K-split launch (``_pf5_split``)."""
+    return G >= 32 and (M <= 64 or (M <= 128 and N <= 4096 and not _pf5_split(M, G, N, K)))
 
 
 def _rows_workgroups(probs) -> int:
