@@ -1258,8 +1258,10 @@ void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t 
 //  * K > 4096 with 64 < M <= 128 (down_proj at M = 128): 64 x 64 tiles of
 //    four parts, K cut into ks ranges of at most 2048 over as many
 //    workgroups while the launch fits one workgroup per CU, finished by the
-//    last range to arrive: down_proj at M = 128 about 14 us against 17 us as
+//    last range to arrive: down_proj at M = 128 15.1 us against 17.1 us as
 //    16-row slices (the decode regime's route for these rows otherwise).
+//    Products of more than 128 rows with at most half a 64 x 64 tile per CU
+//    (k/v at M = 512) take the same split.
 struct Pf5Plan {
   int parts = 0, ts = 64, ks = 1;
 };
@@ -1277,6 +1279,17 @@ Pf5Plan pf5_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
     return p;
   }
   if (G < 64 || K % 128 != 0) return p;
+  if (M > 128 && N % 64 == 0 && K % 2048 == 0 && (M + 63) / 64 * (N / 64) * 2 <= cus) {
+    // at most half a workgroup per CU (k/v at M = 512: 64 tiles): the same
+    // K split, the ranges doubled while they fill more CUs (k/v at M = 512
+    // 10.5 -> 9.5 us with four)
+    int ks = 1;
+    while (2 * ks <= w4::kMaxPf5Split && (M + 63) / 64 * (N / 64) * ks * 2 <= cus && (K / (ks * 2)) % 512 == 0)
+      ks *= 2;
+    p.parts = 4;
+    p.ks = ks;
+    return p;
+  }
   if (N % 64 == 0 && (M + 63) / 64 * (N / 64) <= cus) {
     p.parts = (K % 512 == 0 && M <= N) ? 4 : K % 256 == 0 ? 2 : 1;
     return p;
