@@ -8,10 +8,12 @@ import torch
 
 # (M, N, K, G): decode M=1 (one-CU tiles and narrowed lone tiles), factored
 # decode M=4/16, 32/64-row prefill tiles with split-K (M=32/64), skinny
-# split-K (K % 64 != 0), prefill with split-K (M=128) and without (M=2048)
+# split-K (K % 64 != 0), prefill with split-K (M=128) and without (M=2048),
+# the few-tile prefill kernel's K split across workgroups (M=128 with
+# K=8192, M=512 with N=512)
 CASES = [(1, 2048, 2048, 128), (1, 2048, 8192, 128), (4, 512, 2048, 64), (16, 2048, 2048, 32),
          (32, 8192, 2048, 128), (64, 2048, 8192, 128), (40, 1024, 1032, 8), (128, 2048, 2048, 128),
-         (2048, 2048, 2048, 128)]
+         (2048, 2048, 2048, 128), (128, 2048, 8192, 128), (512, 512, 2048, 128)]
 
 
 def hashes() -> dict:
