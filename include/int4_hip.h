@@ -132,13 +132,13 @@ size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
  * partial tiles, in `workspace`, are summed in part order by the last one to
  * finish); other M <= 64 problems (and group sizes < 32) split-K with fp32
  * partials in `workspace` and a fixed-order reduce kernel; M > 64 tiled
- * MFMA GEMM, itself split over K with the same partials-and-reduce scheme
- * when the shape leaves too few tiles to fill the chip, except that
- * 65 <= M <= 128 with N <= 4096 and dense rows takes the decode kernel's row
- * slices (up to eight) like 17 <= M <= 64, or, for K > 4096, a tiled MFMA
- * launch whose K ranges run in separate workgroups summed in range order by
- * the last one to finish (partial tiles in `workspace`).  Every regime is
- * bit-identical run to run.
+ * MFMA GEMM, itself split over K when the shape leaves too few tiles to fill
+ * the chip: with the same partials-and-reduce scheme, or, for K > 4096 with
+ * few tiles, as K ranges in separate workgroups summed in range order by the
+ * last one to finish (partial tiles in `workspace`); 65 <= M <= 128 with
+ * N <= 4096 and dense rows takes the decode kernel's row slices (up to
+ * eight) like 17 <= M <= 64, except that K > 4096 takes that K-range
+ * launch.  Every regime is bit-identical run to run.
  * Replaces: int4_triton/gemm.py:303-309 (w4a16_matmul) and its dispatcher
  * _matmul, :234-300 (kernels :74-157, :171-182, :185-220).
  */

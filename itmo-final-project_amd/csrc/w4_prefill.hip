@@ -817,7 +817,8 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   uint16_t* const Bs = As + 2 * ASLOT;
   const int wm = wave >> 1, wn = wave & 1;  // this wave's quarter of the tile
   const int l32 = lane & 31, lh = lane >> 5;
-  const int KS = TS == 64 ? a.ks : 1;  // K ranges across workgroups
+  static_assert(TS == 64 || KP == 2, "128-wide tiles run two K parts");
+  const int KS = a.ks;  // K ranges across workgroups
   const int split = KS > 1 ? (int)blockIdx.x / a.tiles_mn : 0;
   const int tb = (int)blockIdx.x - split * a.tiles_mn;  // the tile
   const int tile_m = tb / a.tiles_n;
@@ -988,7 +989,30 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
   __syncthreads();
 
   constexpr int PER = WB * WB * 16;  // accumulator floats per lane
-  if constexpr (KP > 1) {
+  // 128-wide tiles with K cut across workgroups: part p keeps block row
+  // i == p of its wave's 2 x 2 blocks (`own`), so that all eight waves share
+  // the publishing and the last range's reads
+  const bool scattered = TS == 128 && KS > 1;
+  f32x16 own[WB];
+  if constexpr (TS == 128) {
+    if (scattered) {
+      // each part hands the other its other block row through LDS; the sum
+      // p0 + p1 has the same bits in either part (IEEE addition commutes)
+      float* const X = reinterpret_cast<float*>(lds);
+      float* const Xw = X + (kp * 4 + wave) * (WB * 16) * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < WB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) Xw[(j * 16 + e) * 64] = kp == 0 ? acc[1][j][e] : acc[0][j][e];
+      __syncthreads();
+      const float* const Xr = X + ((1 - kp) * 4 + wave) * (WB * 16) * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < WB; ++j)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) own[j][e] = (kp == 0 ? acc[0][j][e] : acc[1][j][e]) + Xr[(j * 16 + e) * 64];
+    }
+  }
+  if (KP > 1 && !scattered) {
     // parts 1..KP-1 -> LDS (lane-major, conflict-free) -> added to part 0 in part
     // order.  Part p's wave w writes its accumulators at P + (p * 4 + w) * PER *
     // 64, element e of the lane at e * 64 + lane (slot 0 unused: every store
@@ -1017,82 +1041,101 @@ __global__ __launch_bounds__(256 * KP) void pf5_kernel(Pf2Args a) {
     }
     __syncthreads();
   }
-  if constexpr (TS == 64) {
-    if (KS > 1) {
-      // K split across workgroups: part 0's waves publish the workgroup's
-      // sum (their accumulators, lane-major 16-byte chunks) with 128-bit
-      // sc1 stores (the cache policy of agent-scope atomic stores: written
-      // through to the level all XCDs share), wait until they have
-      // completed, and count the arrival; the last range to arrive reads the
-      // others with sc1 loads, sums all ranges in range order (so the
-      // result does not depend on which is last), leaves the counter at zero
-      // and writes the tile.
-      constexpr int C = PER / 4;  // 16-byte accumulator chunks per lane
-      float* const parts = a.ws + (int64_t)tb * KS * (TS * TS);
-      const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void*)parts, (short)0,
-                                                                           KS * TS * TS * (int)sizeof(float), 0x00020000);
-      const uint32_t lane_off = ((uint32_t)(wave * C) * 64u + (uint32_t)lane) * 16u;  // + 1024 c
-      constexpr uint32_t RANGE = TS * TS * sizeof(float);
-      if (kp == 0) {
+  if (KS > 1) {
+    // K split across workgroups: the publishing waves (part 0's for 64-wide
+    // tiles, all eight for 128-wide ones) store the workgroup's sum (their
+    // accumulators, lane-major 16-byte chunks) with 128-bit sc1 stores (the
+    // cache policy of agent-scope atomic stores: written through to the
+    // level all XCDs share), wait until they have completed, and count the
+    // arrival; the last range to arrive reads the others with sc1 loads,
+    // sums all ranges in range order (so the result does not depend on which
+    // is last), leaves the counter at zero and writes the tile.
+    constexpr int C = TS == 64 ? PER / 4 : WB * 4;  // 16-byte chunks per publishing lane
+    const bool pub = TS == 128 || kp == 0;
+    const int pw = TS == 128 ? kp * 4 + wave : wave;  // publishing wave
+    f32x4 mine[C];
 #pragma unroll
-        for (int c = 0; c < C; ++c) {
-          const f32x4 v = f32x4{acc[0][0][4 * c], acc[0][0][4 * c + 1], acc[0][0][4 * c + 2], acc[0][0][4 * c + 3]};
-          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
-                                                 (uint32_t)split * RANGE + lane_off + 1024u * c, 0, 16);
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mine[c][e] = TS == 64 ? acc[0][0][4 * c + e] : own[(c / 4) % WB][4 * (c % 4) + e];
+    float* const parts = a.ws + (int64_t)tb * KS * (TS * TS);
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void*)parts, (short)0,
+                                                                         KS * TS * TS * (int)sizeof(float), 0x00020000);
+    const uint32_t lane_off = ((uint32_t)(pw * C) * 64u + (uint32_t)lane) * 16u;  // + 1024 c
+    constexpr uint32_t RANGE = TS * TS * sizeof(float);
+    if (pub) {
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, mine[c]), rp,
+                                               (uint32_t)split * RANGE + lane_off + 1024u * c, 0, 16);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // the arrival count goes through the array's last word, which neither
+    // the part sums (its first half) nor, from here on, the rings use (a
+    // second LDS object made the compiler wait for every direct-to-LDS load
+    // in flight before each fragment read of the main loop)
+    unsigned* const arrived = reinterpret_cast<unsigned*>(lds + KP * SET) - 1;
+    if (threadIdx.x == 0)
+      *arrived = __hip_atomic_fetch_add(a.cnt + tb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*arrived != (unsigned)(KS - 1)) return;
+    if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (pub) {
+      // every other range's chunks are requested before the first add:
+      // slot o holds range o + (o >= split), so the registers are indexed
+      // at compile time
+      u32x4 other[kMaxPf5Split - 1][C];
+#pragma unroll
+      for (int o = 0; o < kMaxPf5Split - 1; ++o)
+        if (o < KS - 1) {
+          const uint32_t q = (uint32_t)(o + (o >= split ? 1 : 0));
+#pragma unroll
+          for (int c = 0; c < C; ++c)
+            other[o][c] = __builtin_amdgcn_raw_buffer_load_b128(rp, q * RANGE + lane_off + 1024u * c, 0, 16);
         }
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-      __syncthreads();
-      // the arrival count goes through the array's last word, which neither
-      // the part sums (its first half) nor, from here on, the rings use (a
-      // second LDS object made the compiler wait for every direct-to-LDS load
-      // in flight before each fragment read of the main loop)
-      unsigned* const arrived = reinterpret_cast<unsigned*>(lds + KP * SET) - 1;
-      if (threadIdx.x == 0)
-        *arrived = __hip_atomic_fetch_add(a.cnt + tb, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __syncthreads();
-      if (*arrived != (unsigned)(KS - 1)) return;
-      if (threadIdx.x == 0) __hip_atomic_store(a.cnt + tb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (kp == 0) {
-        // every other range's chunks are requested before the first add:
-        // slot o holds range o + (o >= split), so the registers are indexed
-        // at compile time
-        u32x4 other[kMaxPf5Split - 1][C];
 #pragma unroll
-        for (int o = 0; o < kMaxPf5Split - 1; ++o)
-          if (o < KS - 1) {
-            const uint32_t q = (uint32_t)(o + (o >= split ? 1 : 0));
+      for (int c = 0; c < C; ++c) {
+        f32x4 sum = mine[c];
 #pragma unroll
-            for (int c = 0; c < C; ++c)
-              other[o][c] = __builtin_amdgcn_raw_buffer_load_b128(rp, q * RANGE + lane_off + 1024u * c, 0, 16);
+        for (int q = 0; q < kMaxPf5Split; ++q) {
+          if (q < KS) {
+            // range q in range order: slot q below this workgroup's range,
+            // slot q - 1 above it (the whole vector is bit-cast: a bit cast
+            // of one element of an ext_vector_type value reads the vector's
+            // first element)
+            const f32x4 below = __builtin_bit_cast(f32x4, other[q < kMaxPf5Split - 1 ? q : 0][c]);
+            const f32x4 above = __builtin_bit_cast(f32x4, other[q > 0 ? q - 1 : 0][c]);
+            const f32x4 t = q < split ? below : q == split ? mine[c] : above;
+            sum = q == 0 ? t : sum + t;
           }
-#pragma unroll
-        for (int c = 0; c < C; ++c) {
-          const f32x4 own = f32x4{acc[0][0][4 * c], acc[0][0][4 * c + 1], acc[0][0][4 * c + 2], acc[0][0][4 * c + 3]};
-          f32x4 sum = own;
-#pragma unroll
-          for (int q = 0; q < kMaxPf5Split; ++q) {
-            if (q < KS) {
-              // range q in range order: slot q below this workgroup's range,
-              // slot q - 1 above it (the whole vector is bit-cast: a bit cast
-              // of one element of an ext_vector_type value reads the vector's
-              // first element)
-              const f32x4 below = __builtin_bit_cast(f32x4, other[q < kMaxPf5Split - 1 ? q : 0][c]);
-              const f32x4 above = __builtin_bit_cast(f32x4, other[q > 0 ? q - 1 : 0][c]);
-              const f32x4 t = q < split ? below : q == split ? own : above;
-              sum = q == 0 ? t : sum + t;
-            }
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[0][0][4 * c + e] = sum[e];
         }
+        mine[c] = sum;
       }
+#pragma unroll
+      for (int c = 0; c < C; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (TS == 64)
+            acc[0][0][4 * c + e] = mine[c][e];
+          else
+            own[(c / 4) % WB][4 * (c % 4) + e] = mine[c][e];
+        }
     }
   }
   // output: the tile in LDS (part 0's area), then 16-byte row chunks
   static_assert(TS * TS <= SET, "output tile fits part 0's area");
   uint16_t* T = lds;
-  if (kp == 0) {
+  if (scattered) {
+    // part p holds block row p of its wave's quarter
+#pragma unroll
+    for (int j = 0; j < WB; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = wm * (TS / 2) + kp * 32 + 8 * (e >> 2) + 4 * lh + (e & 3);
+        T[row * TS + wn * (TS / 2) + j * 32 + l32] = float_to_act_bits<DT>(own[j][e]);
+      }
+  } else if (kp == 0) {
 #pragma unroll
     for (int i = 0; i < WB; ++i)
 #pragma unroll
@@ -1245,9 +1288,10 @@ void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t 
 }
 
 // pf5 (TS x TS tiles, the weight tile dequantized once per workgroup into
-// LDS) for dense rows with group sizes >= 64 (one group per 64-k step) and
-// K <= 4096, a multiple of 128 per K part.  parts = K parts per workgroup
-// (0: not this kernel).
+// LDS) for dense rows with group sizes >= 64 (one group per 64-k step), a
+// multiple of 128 per K part; K <= 4096 unless K is also cut across
+// workgroups (the last two cases).  parts = K parts per workgroup (0: not
+// this kernel).
 //  * TS = 64 where the product has at most one 64 x 64 tile per CU (N % 64
 //    == 0): four parts except for tall products (M > N), which measured
 //    faster with two (k_proj at M = 2048: 13.1 against 14.3 us; q_proj at
@@ -1262,14 +1306,31 @@ void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t 
 //    16-row slices (the decode regime's route for these rows otherwise).
 //    Products of more than 128 rows with at most half a 64 x 64 tile per CU
 //    (k/v at M = 512) take the same split.
+//  * K > 4096 with more than 128 rows and fewer 128 x 128 tiles than CUs
+//    (down_proj at M = 512 / 1024): 128 x 128 tiles of two parts, K cut into
+//    ks = 2 or 4 ranges while the launch fills 3/4 to all of the CUs, each
+//    part keeping half of the tile's sum so that all eight waves share the
+//    last range's reads.
 struct Pf5Plan {
   int parts = 0, ts = 64, ks = 1;
 };
 Pf5Plan pf5_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
   Pf5Plan p;
   const int64_t cus = device_cu_count();
+  if (K > 4096 && M > 128) {
+    const int64_t t128 = (M + 127) / 128 * (N / 128);
+    if (G < 64 || N % 128 != 0) return p;
+    int ks = 2;
+    while (2 * ks <= w4::kMaxPf5Split && t128 * ks * 2 <= cus) ks *= 2;
+    if (t128 * ks <= cus && 4 * t128 * ks >= 3 * cus && K % (256 * ks) == 0) {
+      p.parts = 2;
+      p.ts = 128;
+      p.ks = ks;
+    }
+    return p;
+  }
   if (K > 4096) {
-    if (G < 64 || M <= 64 || M > 128 || N % 64 != 0) return p;
+    if (G < 64 || M <= 64 || N % 64 != 0) return p;
     int ks = 2;
     while (K / ks > 2048) ks *= 2;
     if (ks <= w4::kMaxPf5Split && K % ks == 0 && (K / ks) % 512 == 0 && (M + 63) / 64 * (N / 64) * ks <= cus) {
@@ -1306,7 +1367,7 @@ Pf5Plan pf5_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
 // the plan does not depend on the group size once it is >= 64.
 size_t pf5_split_scratch(int64_t M, int64_t N, int64_t K) {
   const Pf5Plan p = pf5_plan(M, N, K, 64);
-  return p.ks > 1 ? (size_t)p.ks * ((M + 63) / 64) * (N / 64) * 64 * 64 * sizeof(float) : 0;
+  return p.ks > 1 ? (size_t)p.ks * ((M + p.ts - 1) / p.ts) * (N / p.ts) * p.ts * p.ts * sizeof(float) : 0;
 }
 
 template <int DT>

@@ -262,7 +262,10 @@ def test_prefill_group_sizes_and_partial_tiles(M, G, NK):
                                            (2048, 2048, 2048, 128, torch.bfloat16),  # 128 x 128, 256 tiles
                                            (512, 8192, 2048, 256, torch.float16),    # 128 x 128, group 256
                                            (1536, 2048, 1024, 64, torch.float16),    # 128 x 128, 192 tiles, group 64
-                                           (1900, 2048, 768, 128, torch.bfloat16)])  # 128 x 128, ragged M
+                                           (1900, 2048, 768, 128, torch.bfloat16),   # 128 x 128, ragged M
+                                           (512, 2048, 8192, 128, torch.bfloat16),   # 128 x 128, K in 4 ranges
+                                           (700, 2048, 8192, 64, torch.float16),     # 2 ranges, ragged M
+                                           (1024, 1024, 12288, 128, torch.bfloat16)])  # 4 ranges of 3072
 def test_prefill_lds_dequant_tiles(M, N, K, G, dtype):
     from int4_hip import _lib
     print(f"[prefill-lds] M={M} N={N} K={K} G={G} {dtype}", flush=True)
@@ -275,8 +278,11 @@ def test_prefill_lds_dequant_tiles(M, N, K, G, dtype):
     lib = _lib.load()
     xdt = _lib.DTYPE_BF16 if dtype == torch.bfloat16 else _lib.DTYPE_FP16
     ypad = torch.full((M, N + 4), float("nan"), dtype=dtype, device=DEV)
+    nb = lib.w4a16_workspace_bytes(M, N, K, G)  # K split across workgroups: counters and partial tiles
+    ws = torch.zeros(max(nb, 1), dtype=torch.uint8, device=DEV)
     rc = lib.w4a16_gemm(x.data_ptr(), xdt, M, N, K, K, 1, qw.data_ptr(), s.data_ptr(), z.data_ptr(), G,
-                        ypad.data_ptr(), N + 4, None, 0, torch.cuda.current_stream().cuda_stream)
+                        ypad.data_ptr(), N + 4, ws.data_ptr() if nb else None, nb,
+                        torch.cuda.current_stream().cuda_stream)
     _lib.check(rc, "w4a16_gemm")
     torch.cuda.synchronize()
     assert torch.equal(ypad[:, :N].view(torch.int16), out.view(torch.int16))
@@ -366,12 +372,12 @@ def _replays_match(g, out, eager, reps=3):
 # capture on torch's own capture stream after a warm-up on another stream, as
 # eval_llama.py:145-161 (decode step) and triton's do_bench_cudagraph
 # (bench_gemm.py:33-36) do: M = 1 decode shapes whose size query is nonzero,
-# and split-K shapes that need the workspace (M = 128 down_proj and M = 512
-# k_proj: the prefill kernel's K split across workgroups, arrival counters
-# and partial tiles in the workspace)
+# and split-K shapes that need the workspace (M = 128 / 512 down_proj and
+# M = 512 k_proj: the prefill kernel's K split across workgroups, arrival
+# counters and partial tiles in the workspace)
 @pytest.mark.parametrize("M,N,K,G", [(1, 2048, 8192, 128), (1, 2048, 2048, 128), (1, 300, 2048, 16),
                                      (40, 2048, 8192, 128), (64, 8192, 2048, 128), (128, 512, 2048, 128),
-                                     (128, 2048, 8192, 128), (512, 512, 2048, 128)])
+                                     (128, 2048, 8192, 128), (512, 512, 2048, 128), (512, 2048, 8192, 128)])
 def test_capture_without_warmup_on_capture_stream(M, N, K, G):
     print(f"[capture] M={M} N={N} K={K} G={G}", flush=True)
     qw, s, z = _weights(N, K, G, seed=M + N + G)

@@ -34,12 +34,14 @@ def _noalloc(x, qw, s, z):
 #   fp32 split-K partials (prefill kernel with 32/64-row tiles, M <= 64);
 #   the M = 1 decode kernel's K split (long K: partials and arrival counters);
 #   in-kernel split fixup with arrival counters (M = 1, group 16);
-#   prefill split-K at M > 64; the decode kernel, which uses no scratch;
-#   the skinny split-K kernel (strided activation rows)
+#   prefill split-K at M > 64; the prefill kernel's K split across
+#   workgroups on 128 x 128 tiles (2 ranges, then 4); the decode kernel,
+#   which uses no scratch; the skinny split-K kernel (strided activation rows)
 PAIRS = [((64, 8192, 2048, 128), (40, 2048, 2048, 128)),
          ((1, 2048, 8192, 128), (1, 1024, 6144, 64)),
          ((1, 2048, 8192, 16), (1, 300, 2048, 16)),
          ((128, 2048, 8192, 128), (65, 512, 2048, 128)),
+         ((1024, 2048, 8192, 128), (512, 2048, 8192, 128)),
          ((1, 8192, 2048, 128), (1, 512, 2048, 128)),
          ((48, 2048, 4104, 8), (20, 1024, 1032, 8))]
 
