@@ -1308,9 +1308,12 @@ void pf2_launch_g(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t 
 //    (k/v at M = 512) take the same split.
 //  * K > 4096 with more than 128 rows and fewer 128 x 128 tiles than CUs
 //    (down_proj at M = 512 / 1024): 128 x 128 tiles of two parts, K cut into
-//    ks = 2 or 4 ranges while the launch fills 3/4 to all of the CUs, each
-//    part keeping half of the tile's sum so that all eight waves share the
-//    last range's reads.
+//    ks = 2 or 4 ranges of at most 4096 while the launch fills 3/4 to all of
+//    the CUs, each part keeping half of the tile's sum so that all eight
+//    waves share the last range's reads.  Against pf3 (split-K and the
+//    reduce launch): M x N x K = 512 x 2048 x 8192 30.9 vs 34.8 us, 1024 x
+//    2048 x 8192 47.6 vs 50.1, 256 x 4096 x 8192 30.8 vs 34.5, 384 x 2048 x
+//    8192 28.9 vs 31.1; ranges of 7168 (512 x 4096 x 14336) 79.1 vs 72.6.
 struct Pf5Plan {
   int parts = 0, ts = 64, ks = 1;
 };
@@ -1322,7 +1325,7 @@ Pf5Plan pf5_plan(int64_t M, int64_t N, int64_t K, int64_t G) {
     if (G < 64 || N % 128 != 0) return p;
     int ks = 2;
     while (2 * ks <= w4::kMaxPf5Split && t128 * ks * 2 <= cus) ks *= 2;
-    if (t128 * ks <= cus && 4 * t128 * ks >= 3 * cus && K % (256 * ks) == 0) {
+    if (t128 * ks <= cus && 4 * t128 * ks >= 3 * cus && K % (256 * ks) == 0 && K / ks <= 4096) {
       p.parts = 2;
       p.ts = 128;
       p.ks = ks;
