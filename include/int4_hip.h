@@ -133,9 +133,10 @@ size_t w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int group_size);
  * finish); other M <= 64 problems (and group sizes < 32) split-K with fp32
  * partials in `workspace` and a fixed-order reduce kernel; M > 64 tiled
  * MFMA GEMM, itself split over K when the shape leaves too few tiles to fill
- * the chip: with the same partials-and-reduce scheme, or, for K > 4096 with
- * few tiles, as K ranges in separate workgroups summed in range order by the
- * last one to finish (partial tiles in `workspace`); 65 <= M <= 128 with
+ * the chip: with the same partials-and-reduce scheme, or (two splits of
+ * 128 x 256 tiles, and K > 4096 with few tiles) as K ranges in separate
+ * workgroups summed in range order by the last one to finish (partial tiles
+ * in `workspace`); 65 <= M <= 128 with
  * N <= 4096 and dense rows takes the decode kernel's row slices (up to
  * eight) like 17 <= M <= 64, except that K > 4096 takes that K-range
  * launch.  Every regime is bit-identical run to run.

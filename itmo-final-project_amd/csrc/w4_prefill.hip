@@ -228,9 +228,10 @@ struct Pf2Args {
   int M, N, K, gshift;
   int tiles_n, tiles_mn, kt_per_split;
   int y16;  // pf3: y rows 16-byte aligned and N % 8 == 0 (LDS-staged 16-byte output stores)
-  // pf5 with 64 x 64 tiles: K cut into ks ranges over as many workgroups
-  // (workgroup t: range t / tiles_mn of tile t % tiles_mn), finished by the
-  // last to arrive (per-tile arrival counters in cnt, partial tiles in ws)
+  // pf5: K cut into ks ranges over as many workgroups (workgroup t: range
+  // t / tiles_mn of tile t % tiles_mn), finished by the last to arrive
+  // (per-tile arrival counters in cnt, partial tiles in ws); pf3's two-split
+  // finish uses cnt and ws the same way
   int ks;
   unsigned* cnt;
 };
@@ -437,7 +438,7 @@ __device__ __forceinline__ void lds_load16_so(__amdgpu_buffer_rsrc_t r, void* ld
 // grouped q/k/v and gate/up launches at M = 128); with 64- and 128-row tiles
 // the lockstep halves ran no faster than one wave per SIMD, or slower
 // (down_proj at M = 2048: 71 against 68 us).
-template <int DT, int NW, bool SZK, int MB, int KH>
+template <int DT, int NW, bool SZK, int MB, int KH, bool FIN = false>
 __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   typedef typename Act<DT>::frag F;
   static_assert(KH == 1 || KH == 2, "K halves");
@@ -658,7 +659,63 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
   }
 
   constexpr int TW = 64 * NW;  // tile width (elements)
-  if (BM * TW <= 4 * SLOT && a.ws == nullptr && a.y16) {
+  // FIN: K in two splits finished here (arrival counters in a.cnt): both
+  // splits publish their tile (the kh == 0 waves' accumulators, lane-major
+  // 16-byte chunks, as 128-bit sc1 stores: written through to the level all
+  // XCDs share), wait until the stores have completed and count the
+  // arrival; the second to arrive reads the other's tile with sc1 loads,
+  // adds it (p0 + p1 has the same bits in either order), writes y and
+  // leaves the counter at zero.  Otherwise a split writes fp32 partials for
+  // the reduce launch.  (A template parameter: with the finish compiled
+  // into every instantiation, the grouped launches at M = 512 / 2048
+  // measured 7 us slower.)
+  if constexpr (FIN) {
+    constexpr int C = MB * 2 * 4;  // 16-byte accumulator chunks per lane
+    constexpr uint32_t RANGE = BM * TW * sizeof(float);
+    float* const parts = a.ws + (int64_t)tmn * 2 * (BM * TW);
+    const __amdgpu_buffer_rsrc_t rp =
+        __builtin_amdgcn_make_buffer_rsrc((void*)parts, (short)0, 2 * (int)RANGE, 0x00020000);
+    const uint32_t lane_off = ((uint32_t)(wn * C) * 64u + (uint32_t)lane) * 16u;  // + 1024 c
+    if (kh == 0) {
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const f32x4 v = f32x4{acc[c / 8][(c / 4) % 2][4 * (c % 4)], acc[c / 8][(c / 4) % 2][4 * (c % 4) + 1],
+                              acc[c / 8][(c / 4) % 2][4 * (c % 4) + 2], acc[c / 8][(c / 4) % 2][4 * (c % 4) + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
+                                               (uint32_t)split * RANGE + lane_off + 1024u * c, 0, 16);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // the arrival count goes through the ring array's last word (no second
+    // LDS object: that made the compiler wait for every direct-to-LDS load in
+    // flight before the main loop's fragment reads)
+    unsigned* const arrived = reinterpret_cast<unsigned*>(xs_all + KH * 4 * SLOT) - 1;
+    if (tid == 0) *arrived = __hip_atomic_fetch_add(a.cnt + tmn, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (*arrived != 1u) return;
+    if (tid == 0) __hip_atomic_store(a.cnt + tmn, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (kh == 0) {
+      const uint32_t other = (uint32_t)(1 - split) * RANGE;
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {  // two batches of C / 2 loads in flight
+        u32x4 o[C / 2];
+#pragma unroll
+        for (int i = 0; i < C / 2; ++i)
+          o[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, other + lane_off + 1024u * (b * (C / 2) + i), 0, 16);
+#pragma unroll
+        for (int i = 0; i < C / 2; ++i) {
+          const int c = b * (C / 2) + i;
+          const f32x4 t = __builtin_bit_cast(f32x4, o[i]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[c / 8][(c / 4) % 2][4 * (c % 4) + e] += t[e];
+        }
+      }
+    }
+  }
+  // (the conditions below spelled out: a bool variable for them changed the
+  // grouped launch's code, 228 -> 238 VGPRs, and made it slower)
+  if (BM * TW <= 4 * SLOT && (FIN || a.ws == nullptr) && a.y16) {
     // Output through LDS: the tile (BM x 64 NW values of the output dtype,
     // when it fits the four ring slots) is assembled there, then written back
     // as 16-byte chunks, whole 64 NW-wide row segments per 64 NW / 8 lanes
@@ -699,7 +756,7 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + mb * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m >= a.M) continue;
-        if (a.ws != nullptr) {
+        if (!FIN && a.ws != nullptr) {  // fp32 partials for the reduce launch
           float2 v;
           v.x = acc[mb][0][r];
           v.y = acc[mb][1][r];
@@ -714,9 +771,9 @@ __device__ __forceinline__ void pf3_tile(const Pf2Args& a, const int t) {
 }
 
 
-template <int DT, int NW, bool SZK, int MB, int KH>
+template <int DT, int NW, bool SZK, int MB, int KH, bool FIN = false>
 __global__ __launch_bounds__(NW * KH * 64) __attribute__((amdgpu_waves_per_eu(2))) void pf3_kernel(Pf2Args a) {
-  pf3_tile<DT, NW, SZK, MB, KH>(a, (int)blockIdx.x);
+  pf3_tile<DT, NW, SZK, MB, KH, FIN>(a, (int)blockIdx.x);
 }
 
 // Several products sharing one activation matrix (q/k/v, gate/up) in one
@@ -1172,6 +1229,7 @@ namespace {
 
 struct Pf2Plan {
   int nw = 0, mb = 4, kh = 1, splits = 1, kt_per_split = 0, tiles_n = 0, tiles_mn = 0;
+  bool fin = false;  // two K splits finished in the kernel (no reduce launch)
   size_t ws = 0;
 };
 
@@ -1240,6 +1298,14 @@ Pf2Plan plan_pf2(int64_t M, int64_t N, int64_t K, int max_splits = 8, double* t_
     }
   }
   if (t_est != nullptr) *t_est = best_t;
+  // two K splits of the register-staged kernel on 128 x 256 tiles (down_proj
+  // at M = 2048): the second to finish adds the first's tile (partials
+  // [tile][2][128 x 256]; one arrival counter per tile), no reduce launch
+  if (best.splits == 2 && best.nw == 4 && best.mb == 4 && best.kh == 1 && K % w4::PF2_BK == 0 &&
+      (size_t)best.tiles_mn * 4 <= W4_WORKSPACE_COUNTER_BYTES) {
+    best.fin = true;
+    best.ws = (size_t)best.tiles_mn * 2 * (32 * best.mb) * (64 * best.nw) * sizeof(float);
+  }
   return best;
 }
 
@@ -1253,6 +1319,15 @@ bool pf2_ok(const void* x, int64_t M, int64_t N, int64_t K, int64_t sxm, int64_t
 template <int DT, int NW, int MB, int KH>
 void pf3_launch_k(const Pf2Plan& p, bool szk, const w4::Pf2Args& a, hipStream_t st) {
   const dim3 grid((unsigned)(p.tiles_mn * p.splits)), block(NW * KH * 64);
+  if constexpr (NW == 4 && MB == 4 && KH == 1) {
+    if (p.fin) {  // (the plan sets fin for this tiling only)
+      if (szk)
+        hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, true, MB, KH, true>), grid, block, 0, st, a);
+      else
+        hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, false, MB, KH, true>), grid, block, 0, st, a);
+      return;
+    }
+  }
   if (szk)
     hipLaunchKernelGGL((w4::pf3_kernel<DT, NW, true, MB, KH>), grid, block, 0, st, a);
   else
@@ -1461,7 +1536,7 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
       return check_launch("w4a16_gemm (prefill, pf5)");
     }
     const Pf2Plan p = plan_pf2(M, N, K);
-    if (p.ws > 0 && (ws == nullptr || ws_bytes < p.ws))
+    if (p.ws > 0 && (ws == nullptr || ws_bytes < p.ws || (p.fin && counters == nullptr)))
       return fail(W4_ERR_WORKSPACE, "w4a16_gemm: workspace of %zu bytes required, %zu given",
                   (size_t)W4_WORKSPACE_COUNTER_BYTES + p.ws, ws ? ws_bytes : (size_t)0);
     w4::Pf2Args a{};
@@ -1483,6 +1558,7 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
     a.tiles_n = p.tiles_n;
     a.tiles_mn = p.tiles_mn;
     a.kt_per_split = p.kt_per_split;
+    a.cnt = p.fin ? counters : nullptr;
     a.y16 = (N % 8 == 0 && ldy % 8 == 0 && (uintptr_t)y % 16 == 0) ? 1 : 0;
     const bool szk = G < 64;
     if (x_dtype == W4_DTYPE_BF16) {
@@ -1497,7 +1573,7 @@ int w4_prefill_launch(const void* x, int x_dtype, int64_t M, int64_t N, int64_t 
         pf2_launch_g<W4_DTYPE_FP16, 2>(p, szk, a, st);
     }
     int rc = check_launch("w4a16_gemm (prefill)");
-    if (rc != W4_OK || p.splits == 1) return rc;
+    if (rc != W4_OK || p.splits == 1 || p.fin) return rc;
     return w4_splitk_reduce_launch(static_cast<const float*>(ws), p.splits, M, N, x_dtype, y, ldy, st);
   }
   // strided / unaligned activations: the general tile kernel
