@@ -10,10 +10,13 @@ import torch
 # decode M=4/16, 32/64-row prefill tiles with split-K (M=32/64), skinny
 # split-K (K % 64 != 0), prefill with split-K (M=128) and without (M=2048),
 # the few-tile prefill kernel's K split across workgroups (M=128 with
-# K=8192, M=512 with N=512, and 128 x 128 tiles for M=512 with K=8192)
+# K=8192, M=512 with N=512, and 128 x 128 tiles for M=512 with K=8192), and
+# the main prefill kernel's two K splits finished in the kernel (M=2048 with
+# K=8192)
 CASES = [(1, 2048, 2048, 128), (1, 2048, 8192, 128), (4, 512, 2048, 64), (16, 2048, 2048, 32),
          (32, 8192, 2048, 128), (64, 2048, 8192, 128), (40, 1024, 1032, 8), (128, 2048, 2048, 128),
-         (2048, 2048, 2048, 128), (128, 2048, 8192, 128), (512, 512, 2048, 128), (512, 2048, 8192, 128)]
+         (2048, 2048, 2048, 128), (128, 2048, 8192, 128), (512, 512, 2048, 128), (512, 2048, 8192, 128),
+         (2048, 2048, 8192, 128)]
 
 
 def hashes() -> dict:

@@ -372,12 +372,13 @@ def _replays_match(g, out, eager, reps=3):
 # capture on torch's own capture stream after a warm-up on another stream, as
 # eval_llama.py:145-161 (decode step) and triton's do_bench_cudagraph
 # (bench_gemm.py:33-36) do: M = 1 decode shapes whose size query is nonzero,
-# and split-K shapes that need the workspace (M = 128 / 512 down_proj and
-# M = 512 k_proj: the prefill kernel's K split across workgroups, arrival
-# counters and partial tiles in the workspace)
+# and split-K shapes that need the workspace (M = 128 / 512 / 2048 down_proj
+# and M = 512 k_proj: the prefill kernels' K splits finished in the kernel,
+# arrival counters and partial tiles in the workspace)
 @pytest.mark.parametrize("M,N,K,G", [(1, 2048, 8192, 128), (1, 2048, 2048, 128), (1, 300, 2048, 16),
                                      (40, 2048, 8192, 128), (64, 8192, 2048, 128), (128, 512, 2048, 128),
-                                     (128, 2048, 8192, 128), (512, 512, 2048, 128), (512, 2048, 8192, 128)])
+                                     (128, 2048, 8192, 128), (512, 512, 2048, 128), (512, 2048, 8192, 128),
+                                     (2048, 2048, 8192, 128)])
 def test_capture_without_warmup_on_capture_stream(M, N, K, G):
     print(f"[capture] M={M} N={N} K={K} G={G}", flush=True)
     qw, s, z = _weights(N, K, G, seed=M + N + G)
