@@ -255,6 +255,8 @@ SIDE = [  # M, N, K, G, layout
     (2048, 96, 520, 8, "dense"), (300, 8192, 2048, 128, "offset"),
     (33, 73, 2048, 64, "dense"), (100, 300 + 2, 1024, 128, "dense"),  # generic decode kernel in 16-row slices
     (700, 1000, 1024, 64, "dense"), (2048, 520, 2048, 128, "dense"),  # pf3 with a partial last column tile
+    (700, 2048, 8192, 64, "dense"),   # pf5 128 x 128 tiles, K in two ranges, partial last row tile
+    (1900, 2048, 8192, 128, "dense"),  # pf3 two K splits finished in the kernel, partial last row tile
 ]
 
 
